@@ -1,0 +1,254 @@
+"""Benchmark of the flash-attention hot path on one MI355X.
+
+Default workload: non-causal self-attention B=1, H=40, L=32760, D=128 in
+bf16 (Wan2.1-14B 480p, 81 frames; latent grid 21x30x52), inputs ~ N(0,1)
+resident in HBM. One "step" is one call of the kernel over that batch.
+Prints ONE JSON line with the attention TFLOP/s, the fraction of MI355X dense
+bf16 MFMA peak, ms per call, the roofline record of the kernel and a CPU
+baseline timed on this host (the oracle's fp32 restatement on a bounded
+sample of the same workload).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "attention TFLOP/s + % bf16 MFMA peak at L=32760 H=40 D=128; ms/call"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+WORKLOADS = {
+    # name: (kind, params, description)
+    "self_L32760_H40": ("flash", dict(B=1, Sq=32760, Sk=32760, H=40, seed=1),
+                        "self-attention B=1 H=40 L=32760 D=128 (Wan2.1-14B 480p 81f)"),
+    "self_L7800_H12": ("flash", dict(B=1, Sq=7800, Sk=7800, H=12, seed=0),
+                       "self-attention B=1 H=12 L=7800 D=128 (Wan2.1-1.3B)"),
+    "cross_L32760x512_B2": ("flash", dict(B=2, Sq=32760, Sk=512, H=40, seed=2, kv_len=(20, 512)),
+                            "cross-attention B=2 H=40 Lq=32760 Lk=512, kv_len ~ U{20..512}"),
+    "joint_L119056_H24": ("flash", dict(B=1, Sq=119056, Sk=119056, H=24, seed=4, tail_pad=(0, 200)),
+                          "joint self-attention B=1 H=24 S=33*45*80+256, last 0-200 keys masked"),
+    "na3d_21x45x80_H24": ("na3d", dict(B=1, T=21, Hs=45, W=80, NH=24, kernel=(3, 7, 7), seed=3),
+                          "3D neighbourhood attention 21x45x80, window (3,7,7), B=1 NH=24 D=128"),
+}
+DEFAULT_WORKLOAD = "self_L32760_H40"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def _flash_inputs(p, dev):
+    import numpy as np
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(p["seed"])
+    B, Sq, Sk, H = p["B"], p["Sq"], p["Sk"], p["H"]
+    q = torch.randn((B, Sq, H, 128), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((B, Sk, H, 128), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((B, Sk, H, 128), generator=g, device=dev).to(torch.bfloat16)
+    kw = {}
+    valid_keys = [Sk] * B
+    rng = np.random.default_rng(p["seed"])
+    if "kv_len" in p:
+        lo, hi = p["kv_len"]
+        kvl = rng.integers(lo, hi + 1, size=B).astype(np.int32)
+        kw["kv_len"] = torch.from_numpy(kvl).to(dev)
+        valid_keys = [int(x) for x in kvl]
+    if "tail_pad" in p:
+        lo, hi = p["tail_pad"]
+        pad = rng.integers(lo, hi + 1, size=B)
+        valid = torch.ones((B, Sk), dtype=torch.bool, device=dev)
+        for b in range(B):
+            if pad[b]:
+                valid[b, Sk - int(pad[b]):] = False
+        kw["key_valid"] = valid
+        from vidax_amd.attention import _last_valid_plus_one
+        kw["kv_len"] = _last_valid_plus_one(valid)
+        valid_keys = [Sk - int(x) for x in pad]
+    return q, k, v, kw, valid_keys
+
+
+def _flash_work(p, valid_keys):
+    """Algorithmic flops and HBM bytes per call (q, o and the valid k, v once)."""
+    H, D, Sq = p["H"], 128, p["Sq"]
+    flops = 4.0 * H * D * Sq * sum(valid_keys)
+    bytes_ = 2.0 * (p["B"] * Sq * H * D * 2) + 2.0 * sum(valid_keys) * H * D * 2
+    return flops, bytes_
+
+
+def _na3d_work(p):
+    B, T, Hs, W, NH, D = p["B"], p["T"], p["Hs"], p["W"], p["NH"], 128
+    kt, kh, kw = (min(p["kernel"][0], T), min(p["kernel"][1], Hs), min(p["kernel"][2], W))
+    n = T * Hs * W
+    flops = 4.0 * B * NH * n * kt * kh * kw * D
+    bytes_ = 2.0 * 4 * B * n * NH * D
+    return flops, bytes_
+
+
+def _cpu_baseline(kind, p, budget_s=12.0):
+    """Times the oracle's fp32 restatement on a bounded sample of the workload
+    on this host's cores and scales it to the metric's unit (TFLOP/s)."""
+    import numpy as np
+    from oracle import attention_oracle as O
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([d.get("num_threads", 1) for d in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    rng = np.random.default_rng(1234)
+    if kind == "flash":
+        H, Sk = 1, p["Sk"]
+        rows = 1024
+        q = O.bf16_round(rng.standard_normal((1, rows, H, 128), dtype=np.float32))
+        k = O.bf16_round(rng.standard_normal((1, Sk, H, 128), dtype=np.float32))
+        v = O.bf16_round(rng.standard_normal((1, Sk, H, 128), dtype=np.float32))
+        O.attention(q[:, :64], k, v, acc=np.float32)  # warm-up
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            O.attention(q, k, v, acc=np.float32, q_block=256)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or reps >= 64:
+                break
+        flops = 4.0 * 128 * rows * Sk * H * reps
+        sample = (f"oracle fp32 (numpy/BLAS) attention, {reps} x (1 head x {rows} query rows x "
+                  f"{Sk} keys, D=128) of this workload, {el:.1f} s")
+        return {"value": round(flops / el / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads),
+                "kind": "port", "sample": sample}
+    # na3d: a slab of T rows with the full H x W plane, all heads
+    T = min(3, p["T"])
+    shape = (1, T, p["Hs"], p["W"], 2, 128)
+    q = O.bf16_round(rng.standard_normal(shape, dtype=np.float32))
+    k = O.bf16_round(rng.standard_normal(shape, dtype=np.float32))
+    v = O.bf16_round(rng.standard_normal(shape, dtype=np.float32))
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.na3d(q, k, v, p["kernel"], acc=np.float32)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 16:
+            break
+    kt, kh, kw = (min(p["kernel"][0], T), min(p["kernel"][1], p["Hs"]), min(p["kernel"][2], p["W"]))
+    flops = 4.0 * 2 * T * p["Hs"] * p["W"] * kt * kh * kw * 128 * reps
+    sample = f"oracle fp32 NA3D on a (1,{T},{p['Hs']},{p['W']},2,128) slab, {reps} reps, {el:.1f} s"
+    return {"value": round(flops / el / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads),
+            "kind": "port", "sample": sample}
+
+
+def _traffic(kernel_name, workload):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+        return rec.get(workload, {}).get(kernel_name, {}).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs the attention kernels on a single GPU; "
+              "--gpus N with N > 1 is not supported (how the path would shard is "
+              "described in DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+    import vidax_amd
+    from vidax_amd import _lib
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    kind, p, desc = WORKLOADS[args.workload]
+    if kind == "flash":
+        q, k, v, kw, valid_keys = _flash_inputs(p, dev)
+        out = torch.empty_like(q)
+        flops, bytes_ = _flash_work(p, valid_keys)
+
+        def step():
+            vidax_amd.flash_attention(q, k, v, out=out, **kw)
+        kernel_name = "flash_fwd_kernel"
+    else:
+        g = torch.Generator(device=dev)
+        g.manual_seed(p["seed"])
+        shape = (p["B"], p["T"], p["Hs"], p["W"], p["NH"], 128)
+        q = (torch.randn(shape, generator=g, device=dev) * 128 ** -0.5).to(torch.bfloat16)
+        k = torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)
+        out = torch.empty_like(q)
+        flops, bytes_ = _na3d_work(p)
+        from vidax_amd.natten import na3d_attention
+
+        def step():
+            na3d_attention(q, k, v, p["kernel"], out=out)
+        kernel_name = "na3d_fwd_kernel"
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    t0 = time.perf_counter()
+    ev[0].record(stream)
+    for i in range(args.steps):
+        step()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]
+    ms = sum(per) / len(per)
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbs = bytes_ / (ms * 1e-3) / 1e9
+    if kind == "flash":
+        roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                    "traffic": _traffic(kernel_name, args.workload)}
+    else:
+        roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                    "traffic": _traffic(kernel_name, args.workload)}
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = _cpu_baseline(kind, p, args.cpu_budget)
+    rec = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) bf16 inputs resident in HBM",
+        "config": {"workload": desc, "B": p["B"], "heads": p.get("H", p.get("NH")), "head_dim": 128,
+                   "kernel": kernel_name},
+        "pct_bf16_mfma_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
+        "ms_per_call": round(ms, 4),
+        "ms_per_call_min": round(min(per), 4),
+        "algorithmic_gbs": round(gbs, 1),
+        "wall_s": round(wall, 3),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

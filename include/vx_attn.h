@@ -1,0 +1,130 @@
+/*
+ * vx_attn.h -- C ABI of the MI355X (gfx950) attention kernels.
+ *
+ * Plain C: pointers, sizes and a HIP stream passed as an opaque pointer. No
+ * framework types cross this boundary. Every entry point returns VX_OK (0) or
+ * a non-zero VX_ERR_* code; the message for the last failure on the calling
+ * thread is available from vx_last_error(). Nothing throws across the ABI.
+ *
+ * Layouts are the reference's: q/k/v/out are (B, S, H, D) bf16 for the flash
+ * entry point and (B, T, Hs, W, NH, D) bf16 for the neighbourhood entry
+ * point, with D (the head dim) contiguous. The library allocates nothing,
+ * keeps no pointer after returning, never synchronises the stream, and may be
+ * called concurrently from several host threads.
+ */
+#ifndef VX_ATTN_H_
+#define VX_ATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VX_OK 0
+#define VX_ERR_INVALID_ARGUMENT 1 /* shape, stride, alignment, dtype or window error */
+#define VX_ERR_UNSUPPORTED 2      /* a valid request this build has no kernel for   */
+#define VX_ERR_LAUNCH 3           /* the HIP runtime refused the launch             */
+
+/* Version of this ABI (major * 10000 + minor * 100 + patch). */
+int32_t vx_abi_version(void);
+
+/* Message describing the most recent failure on the calling thread ("" if none). */
+const char* vx_last_error(void);
+
+/*
+ * Non-causal flash attention forward:
+ *   out[b, i, h, :] = sum_j softmax_j(scale * q[b,i,h,:] . k[b,j,h,:] + mask_bj) v[b, j, h, :]
+ * with fp32 softmax statistics and fp32 accumulation, bf16 in and out.
+ *
+ * Replaces the reference's flash-attention call sites:
+ *   - src/vidax/core/attention.py:212-288  (_flash_attention_tpu: q/k/v (B,S,H,D),
+ *     sm_scale, zero-padded tails excluded through segment ids at :272-278)
+ *   - src/vidax/core/attention.py:321-338  (local_attention)
+ *   - src/vidax/core/attention.py:467-533  (dot_product_attention, flash branch)
+ *   - src/vidax/models/hunyuan_video/common/dit_layers.py:150-190
+ *     (_flash_attention_tpu_segment_masked: key-only validity mask)
+ *
+ * Key masking (all optional and combined; every one is key-only, i.e. the
+ * same for every query row and every head of a batch item):
+ *   kv_len     int32[B] or NULL: keys j >= kv_len[b] are masked (prefix form,
+ *              the Hunyuan `key_valid` layout; values are clamped to [0, Sk]).
+ *              It also bounds the key loop, so masked tails cost nothing.
+ *   key_valid  uint8[B, key_mask_stride] or NULL: key j of batch b is valid
+ *              iff key_valid[b*key_mask_stride + j] != 0 (general form).
+ *   key_bias   float32[B, key_mask_stride] or NULL: added to the logits of
+ *              key j after scaling; -inf masks the key (Cosmos3's
+ *              (B,1,1,Sk) bias, src/vidax/models/cosmos3/dit_layers.py:124-135).
+ * key_mask_stride is in elements, a multiple of 4 and >= round_up(Sk, 4);
+ * key_valid must be 4-byte and key_bias 16-byte aligned.
+ * A query row whose keys are all masked produces an all-zero output row.
+ *
+ * Strides (element units, {batch, seq, head}) may be NULL for a contiguous
+ * (B, S, H, D) tensor; the head dim must be contiguous. q/k/v/out must be
+ * 16-byte aligned and every stride a multiple of 8 elements.
+ * Supported: head_dim == 128, scale > 0 and finite, 1 <= B, H <= 65535 and
+ * 1 <= Sq, Sk < 2^31.
+ * `stream` is a hipStream_t (NULL = the default stream).
+ */
+int32_t vx_flash_attn_fwd(const void* q, const void* k, const void* v, void* out,
+                          const int32_t* kv_len, const uint8_t* key_valid,
+                          const float* key_bias, int64_t key_mask_stride,
+                          int32_t batch, int32_t seq_q,
+                          int32_t seq_k, int32_t num_heads, int32_t head_dim,
+                          const int64_t* q_strides, const int64_t* k_strides,
+                          const int64_t* v_strides, const int64_t* out_strides, float scale,
+                          void* stream);
+
+/*
+ * Host-only argument check for vx_flash_attn_fwd (no GPU needed): returns what
+ * vx_flash_attn_fwd would return for these arguments before launching.
+ * Pointers are checked for NULL-ness and alignment only.
+ */
+int32_t vx_flash_attn_check(const void* q, const void* k, const void* v, const void* out,
+                            const int32_t* kv_len, const uint8_t* key_valid,
+                            const float* key_bias, int64_t key_mask_stride,
+                            int32_t batch, int32_t seq_q,
+                            int32_t seq_k, int32_t num_heads, int32_t head_dim,
+                            const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides, const int64_t* out_strides,
+                            float scale);
+
+/*
+ * 3D neighbourhood attention forward (NATTEN semantics, boundary-clamped):
+ * for query (t, y, x) the window on each axis is [s, s + K') with
+ * K' = min(K, L) and s = clamp(i - K'/2, 0, L - K'), so every query sees
+ * exactly kt'*kh'*kw' keys and no masking is needed.
+ *   out[b,t,y,x,n,:] = sum_{key in window} softmax(scale * q . k) v
+ * Logits and softmax statistics in fp32; bf16 in and out.
+ *
+ * Replaces src/vidax/models/ltx2_5/diffusion_vae.py:179-234
+ * (neighborhood_attention_3d, whose caller pre-scales q at :265 -- pass
+ * scale = 1.0 for the reference's convention) with window starts as in
+ * diffusion_vae.py:152-164 (_window_start).
+ *
+ * Tensors are contiguous (B, T, Hs, W, NH, D) bf16, 16-byte aligned.
+ * Supported: head_dim in {64, 128}; 1 <= kt, kh, kw; all sizes >= 1.
+ */
+int32_t vx_na3d_fwd(const void* q, const void* k, const void* v, void* out, int32_t batch,
+                    int32_t t, int32_t h, int32_t w, int32_t num_heads, int32_t head_dim,
+                    int32_t kernel_t, int32_t kernel_h, int32_t kernel_w, float scale,
+                    void* stream);
+
+/* Host-only argument check for vx_na3d_fwd (no GPU needed). */
+int32_t vx_na3d_check(const void* q, const void* k, const void* v, const void* out,
+                      int32_t batch, int32_t t, int32_t h, int32_t w, int32_t num_heads,
+                      int32_t head_dim, int32_t kernel_t, int32_t kernel_h, int32_t kernel_w,
+                      float scale);
+
+/*
+ * Failure injection for error-path tests: while `code` is non-zero, every
+ * vx_*_fwd call that passes argument checks returns `code` without launching,
+ * with a message naming the injection. 0 turns it off. Process-wide.
+ */
+void vx_debug_inject_error(int32_t code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VX_ATTN_H_ */

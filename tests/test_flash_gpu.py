@@ -1,0 +1,242 @@
+"""GPU parity tests of the flash-attention kernel against the CPU oracle.
+
+Bar (from the path's specification): max-abs <= 2e-2 and mean-abs <= 2e-3
+against the reference semantics, bf16 in/out with fp32 softmax statistics.
+Each test also checks the error relative to the output RMS, which catches
+mistakes that the absolute bound alone would let through on tiny outputs.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_ABS = 2e-3
+MEAN_REL_RMS = 1e-2  # mean-abs error / RMS(reference)
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _t(x, dev):
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(dev).to(torch.bfloat16)
+
+
+def _errs(out, ref):
+    o = out.float().cpu().numpy().astype(np.float64)
+    d = np.abs(o - ref)
+    rms = float(np.sqrt(np.mean(ref ** 2))) + 1e-30
+    return float(d.max()), float(d.mean()), float(d.mean()) / rms
+
+
+def _check(out, ref, label):
+    mx, mean, rel = _errs(out, ref)
+    print(f"  {label}: max_abs={mx:.3e} mean_abs={mean:.3e} mean/rms={rel:.3e}", flush=True)
+    assert np.isfinite(out.float().cpu().numpy()).all(), f"{label}: non-finite output"
+    assert mx <= MAX_ABS, f"{label}: max-abs {mx}"
+    assert mean <= MEAN_ABS, f"{label}: mean-abs {mean}"
+    assert rel <= MEAN_REL_RMS, f"{label}: mean-abs/rms {rel}"
+
+
+SMALL_CASES = [
+    # B, Sq, Sk, H, seed, mask
+    (1, 128, 128, 2, 10, None),
+    (1, 64, 64, 1, 11, None),
+    (2, 200, 300, 3, 12, None),          # ragged query and key tails
+    (1, 1, 1, 1, 13, None),
+    (1, 257, 1, 2, 14, None),            # Sk = 1: out = v
+    (1, 33, 65, 2, 15, None),
+    (1, 300, 1000, 2, 16, None),         # several key tiles + tail 40
+    (3, 100, 777, 2, 17, ("kv_len", 0, 777)),
+    (2, 130, 512, 4, 18, ("kv_len", 20, 512)),   # the cross-attention regime
+    (2, 96, 515, 2, 19, ("tail_pad", 0, 200)),   # joint text+video padding
+]
+
+
+@pytest.mark.parametrize("B,Sq,Sk,H,seed,mask", SMALL_CASES)
+def test_flash_small(gpu, B, Sq, Sk, H, seed, mask):
+    from vidax_amd import flash_attention
+    _say(f"flash small B={B} Sq={Sq} Sk={Sk} H={H} seed={seed} mask={mask}")
+    q, k, v, extra = O.make_flash_inputs(B, Sq, Sk, H, 128, seed, mask)
+    kw = {}
+    if "kv_len" in extra:
+        kw["kv_len"] = torch.from_numpy(extra["kv_len"]).to(gpu)
+    if "key_valid" in extra:
+        kw["key_valid"] = torch.from_numpy(extra["key_valid"]).to(gpu)
+    out = flash_attention(_t(q, gpu), _t(k, gpu), _t(v, gpu), **kw)
+    torch.cuda.synchronize()
+    ref = O.attention(q, k, v, kv_len=extra.get("kv_len"), key_valid=extra.get("key_valid"))
+    _check(out, ref, "oracle")
+
+
+def test_flash_sk1_returns_v(gpu):
+    """Sk = 1: every query attends one key with weight 1, so out = v."""
+    from vidax_amd import flash_attention
+    _say("flash Sk=1 identity")
+    q, k, v, _ = O.make_flash_inputs(2, 70, 1, 3, 128, 20)
+    out = flash_attention(_t(q, gpu), _t(k, gpu), _t(v, gpu)).float().cpu().numpy()
+    np.testing.assert_array_equal(out, np.broadcast_to(v, out.shape))
+
+
+def test_flash_fully_masked_rows_are_zero(gpu):
+    from vidax_amd import flash_attention
+    _say("flash fully masked batch item")
+    q, k, v, _ = O.make_flash_inputs(2, 50, 130, 2, 128, 21)
+    kv_len = torch.tensor([0, 130], dtype=torch.int32, device=gpu)
+    out = flash_attention(_t(q, gpu), _t(k, gpu), _t(v, gpu), kv_len=kv_len)
+    o = out.float().cpu().numpy()
+    assert (o[0] == 0).all()
+    ref = O.attention(q[1:], k[1:], v[1:])
+    _check(out[1:], ref, "unmasked item")
+
+
+def test_flash_general_key_mask_and_bias(gpu):
+    """key_valid with holes and an additive key bias with -inf entries."""
+    from vidax_amd import flash_attention
+    _say("flash key_valid holes + key_bias")
+    rng = np.random.default_rng(22)
+    B, Sq, Sk, H = 2, 150, 333, 2
+    q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, 128, 22)
+    valid = rng.random((B, Sk)) > 0.3
+    bias = rng.standard_normal((B, Sk)).astype(np.float32)
+    bias[rng.random((B, Sk)) < 0.1] = -np.inf
+    tq, tk, tv = _t(q, gpu), _t(k, gpu), _t(v, gpu)
+    out = flash_attention(tq, tk, tv, key_valid=torch.from_numpy(valid).to(gpu))
+    _check(out, O.attention(q, k, v, key_valid=valid), "key_valid")
+    out = flash_attention(tq, tk, tv, key_bias=torch.from_numpy(bias).to(gpu))
+    _check(out, O.attention(q, k, v, key_bias=bias), "key_bias")
+    kv_len = np.array([100, 333], dtype=np.int32)
+    out = flash_attention(tq, tk, tv, key_valid=torch.from_numpy(valid).to(gpu),
+                          key_bias=torch.from_numpy(bias).to(gpu),
+                          kv_len=torch.from_numpy(kv_len).to(gpu))
+    _check(out, O.attention(q, k, v, key_valid=valid, key_bias=bias, kv_len=kv_len), "all three")
+
+
+def test_flash_scale_and_strided_views(gpu):
+    """scale = 1.0 (T5 convention) and q/k/v taken as views of a fused qkv tensor."""
+    from vidax_amd import flash_attention
+    _say("flash scale=1 strided views")
+    B, S, H, D = 2, 190, 3, 128
+    rng = np.random.default_rng(23)
+    qkv = O.bf16_round(rng.standard_normal((B, S, 3, H, D), dtype=np.float32) * np.float32(0.2))
+    t = _t(qkv, gpu)
+    q, k, v = t[:, :, 0], t[:, :, 1], t[:, :, 2]
+    assert not q.is_contiguous()
+    out = flash_attention(q, k, v, scale=1.0)
+    ref = O.attention(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], scale=1.0)
+    _check(out, ref, "strided")
+    out2 = flash_attention(q.contiguous(), k.contiguous(), v.contiguous(), scale=1.0)
+    assert torch.equal(out, out2)
+
+
+def test_flash_deterministic(gpu):
+    from vidax_amd import flash_attention
+    _say("flash determinism")
+    q, k, v, _ = O.make_flash_inputs(1, 500, 700, 4, 128, 24)
+    tq, tk, tv = _t(q, gpu), _t(k, gpu), _t(v, gpu)
+    a = flash_attention(tq, tk, tv)
+    b = flash_attention(tq, tk, tv)
+    assert torch.equal(a, b)
+
+
+def test_flash_config1_full(gpu):
+    """Wan2.1-1.3B self-attention, B=1 H=12 L=7800 D=128, seed 0, whole output."""
+    from vidax_amd import flash_attention
+    _say("flash c1 full B=1 H=12 L=7800")
+    q, k, v, _ = O.make_flash_inputs(1, 7800, 7800, 12, 128, 0)
+    out = flash_attention(_t(q, gpu), _t(k, gpu), _t(v, gpu))
+    ref = O.attention(q, k, v, acc=np.float32)
+    _check(out, ref, "c1")
+
+
+def _rows(n_total, n, seed):
+    rng = np.random.default_rng(seed)
+    rows = rng.choice(n_total, size=n, replace=False)
+    rows[:2] = [0, n_total - 1]
+    return np.sort(rows)
+
+
+def _torch_inputs(B, Sq, Sk, H, seed, dev):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q = torch.randn((B, Sq, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    k = torch.randn((B, Sk, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    v = torch.randn((B, Sk, H, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    return q, k, v
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.slow
+def test_flash_config2_sampled_rows(gpu):
+    """Headline shape B=1 H=40 L=32760: 160 sampled query rows (all heads) vs the oracle."""
+    from vidax_amd import flash_attention
+    _say("flash c2 B=1 H=40 L=32760 sampled rows")
+    q, k, v = _torch_inputs(1, 32760, 32760, 40, 1, gpu)
+    out = flash_attention(q, k, v)
+    rows = _rows(32760, 160, 1)
+    ref = O.attention_rows(_np(q), _np(k), _np(v), rows)
+    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, "c2 rows")
+
+
+@pytest.mark.slow
+def test_flash_config3_cross_kvlen(gpu):
+    """Cross attention Lq=32760, Lk=512, B=2 H=40, kv_len ~ U{20..512}."""
+    from vidax_amd import flash_attention
+    _say("flash c3 cross B=2 H=40 Lq=32760 Lk=512 kv_len")
+    q, k, v = _torch_inputs(2, 32760, 512, 40, 2, gpu)
+    kv_len = np.random.default_rng(2).integers(20, 513, size=2).astype(np.int32)
+    out = flash_attention(q, k, v, kv_len=torch.from_numpy(kv_len).to(gpu))
+    rows = _rows(32760, 512, 2)
+    ref = O.attention_rows(_np(q), _np(k), _np(v), rows, kv_len=kv_len)
+    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, "c3 rows")
+    # the same mask as a boolean key mask through dot_product_attention
+    from vidax_amd import dot_product_attention
+    valid = torch.arange(512, device=gpu)[None, :] < torch.from_numpy(kv_len).to(gpu)[:, None]
+    out2 = dot_product_attention(q, k, v, mask=valid[:, None, None, :])
+    assert torch.equal(out, out2)
+
+
+@pytest.mark.slow
+def test_flash_config5_joint_sampled_rows(gpu):
+    """Joint text+video B=1 H=24, S = 33*45*80 + 256 = 119056, last p ~ U{0..200} keys invalid."""
+    from vidax_amd import masked_self_attention
+    _say("flash c5 joint B=1 H=24 S=119056 key padding")
+    S = 33 * 45 * 80 + 256
+    q, k, v = _torch_inputs(1, S, S, 24, 4, gpu)
+    p = int(np.random.default_rng(4).integers(0, 201))
+    valid = torch.ones((1, S), dtype=torch.bool, device=gpu)
+    if p:
+        valid[:, S - p:] = False
+    out = masked_self_attention(q, k, v, key_valid=valid).reshape(1, S, 24, 128)
+    rows = _rows(S, 48, 4)
+    ref = O.attention_rows(_np(q), _np(k), _np(v), rows, key_valid=_np(valid).astype(bool))
+    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"c5 rows (p={p})")
+
+
+@pytest.mark.slow
+def test_flash_config5_zero_query_is_valid_mean(gpu):
+    """Full-size invariant: q = 0 gives uniform weights, so every output row is
+    the mean of the valid V rows (pins masking, accumulation over all 119k
+    keys and the normalisation, independently of the oracle)."""
+    from vidax_amd import flash_attention
+    _say("flash c5 q=0 mean-of-valid-V invariant")
+    S = 33 * 45 * 80 + 256
+    _, k, v = _torch_inputs(1, 256, S, 24, 5, gpu)
+    q = torch.zeros((1, 256, 24, 128), dtype=torch.bfloat16, device=gpu)
+    n_valid = S - 137
+    out = flash_attention(q, k, v, kv_len=torch.tensor([n_valid], dtype=torch.int32, device=gpu))
+    mean = v[:, :n_valid].double().mean(dim=1, keepdim=True)  # (1, 1, H, D)
+    err = (out.double() - mean).abs()
+    print(f"  max_abs={err.max().item():.3e}", flush=True)
+    # all weights are exactly 1 in bf16; only fp32 accumulation and the bf16
+    # rounding of a ~3e-3-sized output remain
+    assert err.max().item() <= 1e-4

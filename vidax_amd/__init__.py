@@ -1,0 +1,19 @@
+"""vidax_amd: MI355X (gfx950) HIP kernels for vidax's DiT attention hot path.
+
+Drop-in replacements for the reference's attention entry points:
+  dot_product_attention, local_attention   (src/vidax/core/attention.py)
+  masked_self_attention                   (src/vidax/models/hunyuan_video/common/dit_layers.py)
+  neighborhood_attention_3d               (src/vidax/models/ltx2_5/diffusion_vae.py)
+all backed by libvx_attn.so (C ABI: include/vx_attn.h).
+"""
+from .attention import (dot_product_attention, flash_attention, local_attention,
+                        masked_self_attention)
+from .natten import neighborhood_attention_3d
+
+__all__ = [
+    "dot_product_attention",
+    "flash_attention",
+    "local_attention",
+    "masked_self_attention",
+    "neighborhood_attention_3d",
+]

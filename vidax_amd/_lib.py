@@ -1,0 +1,104 @@
+"""ctypes binding of libvx_attn.so (the C ABI in include/vx_attn.h).
+
+torch is imported before the library is opened so that the library binds to
+the HIP runtime torch already loaded (both resolve `libamdhip64.so.7`): device
+pointers and the hipStream_t taken from torch are then valid in the kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must precede the dlopen below)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvx_attn.so")
+
+VX_OK = 0
+VX_ERR_INVALID_ARGUMENT = 1
+VX_ERR_UNSUPPORTED = 2
+VX_ERR_LAUNCH = 3
+
+EXPORTED_SYMBOLS = (
+    "vx_abi_version",
+    "vx_last_error",
+    "vx_flash_attn_fwd",
+    "vx_flash_attn_check",
+    "vx_na3d_fwd",
+    "vx_na3d_check",
+    "vx_debug_inject_error",
+)
+
+_lock = threading.Lock()
+_lib = None
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+_FLASH_ARGS = [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32,
+               _i64p, _i64p, _i64p, _i64p, _f32]
+_NA3D_ARGS = [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32]
+
+
+class VxError(RuntimeError):
+    """A failure reported by the C ABI (code and message from vx_last_error)."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"vx error {code}: {message}")
+        self.code = code
+        self.message = message
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"vidax_amd: {LIB_PATH} is missing; build it with "
+                    "`python -m vidax_amd.build` (or __graft_entry__.build()). "
+                    "There is no fallback implementation.")
+            h = ctypes.CDLL(LIB_PATH)
+            h.vx_abi_version.restype = _i32
+            h.vx_abi_version.argtypes = []
+            h.vx_last_error.restype = ctypes.c_char_p
+            h.vx_last_error.argtypes = []
+            h.vx_flash_attn_fwd.restype = _i32
+            h.vx_flash_attn_fwd.argtypes = _FLASH_ARGS + [_p]
+            h.vx_flash_attn_check.restype = _i32
+            h.vx_flash_attn_check.argtypes = _FLASH_ARGS
+            h.vx_na3d_fwd.restype = _i32
+            h.vx_na3d_fwd.argtypes = _NA3D_ARGS + [_p]
+            h.vx_na3d_check.restype = _i32
+            h.vx_na3d_check.argtypes = _NA3D_ARGS
+            h.vx_debug_inject_error.restype = None
+            h.vx_debug_inject_error.argtypes = [_i32]
+            _lib = h
+    return _lib
+
+
+def last_error() -> str:
+    return lib().vx_last_error().decode("utf-8", "replace")
+
+
+def raise_for(code: int) -> None:
+    """Maps a non-zero C ABI return code to a Python exception."""
+    if code == VX_OK:
+        return
+    msg = last_error()
+    if code == VX_ERR_INVALID_ARGUMENT:
+        raise ValueError(f"vidax_amd: {msg}")
+    if code == VX_ERR_UNSUPPORTED:
+        raise NotImplementedError(f"vidax_amd: {msg}")
+    raise VxError(code, msg)
+
+
+def strides3(strides) -> ctypes.Array:
+    arr = (ctypes.c_int64 * 3)(*[int(s) for s in strides])
+    return arr

@@ -1,0 +1,228 @@
+"""Attention entry points of vidax, re-exposed over the gfx950 HIP kernels.
+
+Same names, arguments, layouts and masking semantics as the reference's
+`src/vidax/core/attention.py` and `src/vidax/models/hunyuan_video/common/
+dit_layers.py`, with torch tensors on the GPU standing in for jnp arrays
+(q/k/v are (B, S, H, D) bfloat16 cuda tensors). Every call launches the HIP
+kernel through the C ABI on torch's current stream; there is no other
+implementation behind these functions, so a missing library or an unsupported
+request raises instead of silently running something else.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "flash_attention",
+    "local_attention",
+    "dot_product_attention",
+    "masked_self_attention",
+]
+
+
+def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be (B, S, H, D); got shape {tuple(t.shape)}")
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be bfloat16; got {t.dtype}")
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be a GPU tensor")
+        if t.stride(-1) != 1:
+            raise ValueError(f"{name} must have a contiguous head dim")
+    if k.shape != v.shape:
+        raise ValueError(f"k and v shapes differ: {tuple(k.shape)} vs {tuple(v.shape)}")
+    if q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2] or q.shape[3] != k.shape[3]:
+        raise ValueError(f"q {tuple(q.shape)} and k {tuple(k.shape)} disagree on B, H or D")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("q, k and v must be on the same device")
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """Tensor usable by the kernels: 16-byte aligned with strides in multiples of 8."""
+    if t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:3]):
+        return t
+    return t.contiguous()
+
+
+def _mask_rows(x: torch.Tensor, sk: int, dtype: torch.dtype, fill) -> torch.Tensor:
+    """(B, Sk) -> (B, round_up(Sk, 4)) contiguous copy in `dtype`, padded with `fill`."""
+    b = x.shape[0]
+    width = (sk + 3) // 4 * 4
+    out = torch.full((b, width), fill, dtype=dtype, device=x.device)
+    out[:, :sk] = x.to(dtype)
+    return out
+
+
+def _last_valid_plus_one(valid: torch.Tensor) -> torch.Tensor:
+    """(B, Sk) bool -> int32 (B,) index of the last valid key + 1 (0 if none), on device."""
+    sk = valid.shape[-1]
+    pos = torch.arange(1, sk + 1, device=valid.device, dtype=torch.int32)
+    return (valid.to(torch.int32) * pos).amax(dim=-1).to(torch.int32).contiguous()
+
+
+def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+                    scale: Optional[float] = None,
+                    kv_len: Optional[torch.Tensor] = None,
+                    key_valid: Optional[torch.Tensor] = None,
+                    key_bias: Optional[torch.Tensor] = None,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Non-causal flash attention with optional key-only masks.
+
+    q (B, Sq, H, D), k/v (B, Sk, H, D), bf16 on the GPU; returns (B, Sq, H, D).
+    scale defaults to 1/sqrt(D) (`src/vidax/core/attention.py:335,524`).
+    kv_len (B,) int: keys >= kv_len[b] masked (prefix form). key_valid
+    (B, Sk) bool/int: general key validity. key_bias (B, Sk) float: additive
+    logits (-inf masks). All masks broadcast over heads and query rows, as
+    the reference's segment ids do (`hunyuan_video/common/dit_layers.py:183-186`).
+    """
+    _check_qkv(q, k, v)
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    if scale is None:
+        scale = D ** -0.5
+    scale = float(scale)
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    if out is None:
+        out = torch.empty((B, Sq, H, D), dtype=q.dtype, device=q.device)
+    elif out.shape != (B, Sq, H, D) or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise ValueError("out must be a (B, Sq, H, D) bf16 tensor with a contiguous head dim")
+    dev = q.device
+    kv_len_t = key_valid_t = key_bias_t = None
+    stride = 0
+    if kv_len is not None:
+        kv_len_t = torch.as_tensor(kv_len, device=dev).to(torch.int32).reshape(B).contiguous()
+    if key_valid is not None:
+        kvd = torch.as_tensor(key_valid, device=dev).reshape(B, Sk).to(torch.bool)
+        key_valid_t = _mask_rows(kvd, Sk, torch.uint8, 0)
+        stride = key_valid_t.shape[1]
+    if key_bias is not None:
+        kbd = torch.as_tensor(key_bias, device=dev).reshape(B, Sk).to(torch.float32)
+        key_bias_t = _mask_rows(kbd, Sk, torch.float32, float("-inf"))
+        stride = key_bias_t.shape[1]
+    L = _lib.lib()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    with torch.cuda.device(dev):
+        rc = L.vx_flash_attn_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            kv_len_t.data_ptr() if kv_len_t is not None else None,
+            key_valid_t.data_ptr() if key_valid_t is not None else None,
+            key_bias_t.data_ptr() if key_bias_t is not None else None,
+            stride, B, Sq, Sk, H, D,
+            _lib.strides3(q.stride()[:3]), _lib.strides3(k.stride()[:3]),
+            _lib.strides3(v.stride()[:3]), _lib.strides3(out.stride()[:3]),
+            ctypes.c_float(scale), ctypes.c_void_p(stream))
+    _lib.raise_for(rc)
+    return out
+
+
+def _single_device(mesh) -> None:
+    """This build runs on one GPU: a mesh, if given, must hold one device."""
+    if mesh is None:
+        return
+    size = getattr(mesh, "size", None)
+    devices = getattr(mesh, "devices", None)
+    if size is None and devices is not None:
+        size = getattr(devices, "size", None)
+    if size != 1:
+        raise NotImplementedError(
+            "vidax_amd runs attention on a single GPU; multi-device meshes "
+            "(the reference's shard_map wrappers) are not part of this build")
+
+
+def _key_only(x: torch.Tensor, B: int, Sk: int, what: str) -> Optional[torch.Tensor]:
+    """Reduces a tensor broadcastable to (B, H, Sq, Sk) to (B, Sk) if it only
+    varies along batch and key; returns None otherwise."""
+    x = torch.as_tensor(x)
+    while x.dim() < 4:
+        x = x.unsqueeze(0)
+    if x.dim() != 4:
+        raise ValueError(f"{what} must be broadcastable to (B, H, Sq, Sk)")
+    if x.shape[1] != 1 or x.shape[2] != 1:
+        return None
+    return x.expand(B, 1, 1, Sk).reshape(B, Sk)
+
+
+def local_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    scale: Optional[float] = None) -> torch.Tensor:
+    """Plain single-call attention (`src/vidax/core/attention.py:321-338`)."""
+    head_dim = q.shape[-1]
+    sm_scale = head_dim ** -0.5 if scale is None else scale
+    return flash_attention(q, k, v, scale=sm_scale)
+
+
+def dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                          bias: Optional[torch.Tensor] = None,
+                          mask: Optional[torch.Tensor] = None,
+                          scale: Optional[float] = None,
+                          mesh=None) -> torch.Tensor:
+    """Full non-causal attention (`src/vidax/core/attention.py:467-533`).
+
+    `bias` and `mask` are broadcastable to (B, H, Sq, Sk), as in the
+    reference. Key-only forms -- shape (B or 1, 1, 1, Sk), e.g. Cosmos3's
+    (B, 1, 1, Sk) -inf padding bias -- run in the flash kernel (the masked
+    key loop is bounded by the last valid key). Head- or query-dependent
+    biases and masks (T5 relative bias, causal masks) take the reference's
+    materialising fallback there; that path is not part of this build and
+    raises NotImplementedError.
+    """
+    _check_qkv(q, k, v)
+    _single_device(mesh)
+    B, _, _, D = q.shape
+    Sk = k.shape[1]
+    sm_scale = D ** -0.5 if scale is None else scale
+    key_bias = key_valid = kv_len = None
+    valid = None
+    if bias is not None:
+        kb = _key_only(torch.as_tensor(bias, device=q.device), B, Sk, "bias")
+        if kb is None:
+            raise NotImplementedError(
+                "head- or query-dependent attention bias is not supported by the "
+                "flash kernel (the reference materialises it in XLA)")
+        key_bias = kb.to(torch.float32)
+        valid = key_bias > float("-inf")
+    if mask is not None:
+        km = _key_only(torch.as_tensor(mask, device=q.device), B, Sk, "mask")
+        if km is None:
+            raise NotImplementedError(
+                "head- or query-dependent boolean masks are not supported by the "
+                "flash kernel (the reference materialises them in XLA)")
+        key_valid = km.to(torch.bool)
+        valid = key_valid if valid is None else (valid & key_valid)
+    if valid is not None:
+        kv_len = _last_valid_plus_one(valid)
+    return flash_attention(q, k, v, scale=sm_scale, kv_len=kv_len, key_valid=key_valid,
+                           key_bias=key_bias)
+
+
+def masked_self_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                          key_valid: Optional[torch.Tensor] = None,
+                          mesh=None, tp_sharded: bool = True) -> torch.Tensor:
+    """Self-attention with an optional key-only validity mask, returning
+    (B, S, H*D) (`src/vidax/models/hunyuan_video/common/dit_layers.py:264-337`).
+
+    key_valid (B, S) bool/int marks valid keys; every query row (valid or
+    not) attends exactly the valid keys, as the reference's segment ids do
+    (q ids all 1, kv ids = key_valid; `dit_layers.py:183-186`). The reference
+    documents valid keys as a prefix; any pattern is handled exactly here,
+    and the key loop stops at the last valid key.
+    """
+    del tp_sharded  # selects a shard_map wrapper in the reference; one GPU here
+    _check_qkv(q, k, v)
+    _single_device(mesh)
+    b, s, h, d = q.shape
+    scale = 1.0 / math.sqrt(d)
+    if key_valid is None:
+        out = flash_attention(q, k, v, scale=scale)
+    else:
+        kv = torch.as_tensor(key_valid, device=q.device).reshape(b, k.shape[1]).to(torch.bool)
+        out = flash_attention(q, k, v, scale=scale, kv_len=_last_valid_plus_one(kv), key_valid=kv)
+    return out.reshape(b, s, h * d)

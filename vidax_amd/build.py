@@ -1,0 +1,77 @@
+"""Build recipe for libvx_attn.so (gfx950 HIP kernels + the C ABI).
+
+Compiles in-tree so the shared library sits next to the package:
+  * vx_capi.cpp with g++ (host-only argument checks and error reporting),
+  * every *.hip file with hipcc --offload-arch=gfx950,
+  * links them into vidax_amd/libvx_attn.so with hipcc.
+
+Run `python -m vidax_amd.build` or call build_library().
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(PKG_DIR, "csrc")
+BUILD_DIR = os.path.join(PKG_DIR, "_build")
+LIB_PATH = os.path.join(PKG_DIR, "libvx_attn.so")
+ARCH = "gfx950"
+
+# Packed FP32 VALU forms are kept out of the generated code.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    lines = [ln for ln in res.stdout.splitlines() if "packed-fp32-ops" not in ln]
+    if res.returncode != 0:
+        raise RuntimeError(f"build step failed ({res.returncode}): {' '.join(cmd)}\n" + "\n".join(lines))
+    return "\n".join(lines)
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compile every source and link libvx_attn.so; returns the library path."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    hipcc = _hipcc()
+    jobs = []
+    objs = []
+    for name in sorted(os.listdir(CSRC)):
+        src = os.path.join(CSRC, name)
+        obj = os.path.join(BUILD_DIR, name + ".o")
+        if name.endswith(".hip"):
+            jobs.append([hipcc, *HIP_FLAGS, "-c", src, "-o", obj])
+        elif name.endswith(".cpp"):
+            jobs.append(["g++", *CXX_FLAGS, "-c", src, "-o", obj])
+        else:
+            continue
+        objs.append(obj)
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
+        for out in ex.map(lambda c: _run(c, verbose), jobs):
+            if verbose and out:
+                print(out)
+    tmp = LIB_PATH + ".tmp"
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build_library(verbose="-v" in sys.argv))

@@ -1,0 +1,225 @@
+// C ABI of the attention kernels (declared in include/vx_attn.h).
+//
+// Plain C++ with no HIP dependency: argument checks, error reporting and the
+// failure-injection hook run on a host without a GPU. The kernels are reached
+// through vx::launch_* (flash_fwd.hip, na3d_fwd.hip).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <atomic>
+#include <cmath>
+
+#include "../../include/vx_attn.h"
+#include "vx_kernels.h"
+
+namespace {
+
+thread_local char g_error[512] = "";
+std::atomic<int32_t> g_inject{0};
+
+int32_t fail(int32_t code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int32_t ok() {
+  g_error[0] = '\0';
+  return VX_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Fills s[3] with the given strides or the contiguous (B, S, H, D) ones.
+void strides_or_default(const int64_t* given, int32_t S, int32_t H, int32_t D, int64_t s[3]) {
+  if (given != nullptr) {
+    s[0] = given[0];
+    s[1] = given[1];
+    s[2] = given[2];
+  } else {
+    s[2] = D;
+    s[1] = (int64_t)H * D;
+    s[0] = (int64_t)S * H * D;
+  }
+}
+
+int32_t check_strides(const char* name, const int64_t s[3], int32_t S) {
+  for (int i = 0; i < 3; ++i) {
+    if (s[i] < 0) return fail(VX_ERR_INVALID_ARGUMENT, "%s stride[%d] = %lld is negative", name, i, (long long)s[i]);
+    if (s[i] % 8 != 0)
+      return fail(VX_ERR_INVALID_ARGUMENT, "%s stride[%d] = %lld is not a multiple of 8 elements", name, i,
+                  (long long)s[i]);
+  }
+  (void)S;  // row offsets are formed in 64-bit inside the kernels
+  return VX_OK;
+}
+
+int32_t flash_check(const void* q, const void* k, const void* v, const void* out, const int32_t* kv_len,
+                    const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride, int32_t B,
+                    int32_t Sq, int32_t Sk,
+                    int32_t H, int32_t D, const int64_t* qs_in, const int64_t* ks_in, const int64_t* vs_in,
+                    const int64_t* os_in, float scale, vx::FlashArgs* args) {
+  (void)kv_len;
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr)
+    return fail(VX_ERR_INVALID_ARGUMENT, "q, k, v and out must be non-NULL");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(VX_ERR_INVALID_ARGUMENT, "q, k, v and out must be 16-byte aligned");
+  if (B < 1 || Sq < 1 || Sk < 1 || H < 1)
+    return fail(VX_ERR_INVALID_ARGUMENT, "batch (%d), seq_q (%d), seq_k (%d) and num_heads (%d) must be >= 1", B, Sq,
+                Sk, H);
+  if (B > 65535 || H > 65535)
+    return fail(VX_ERR_INVALID_ARGUMENT, "batch (%d) and num_heads (%d) must be <= 65535", B, H);
+  if (D != 128) return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 128)", D);
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(VX_ERR_INVALID_ARGUMENT, "scale must be positive and finite (got %g)", (double)scale);
+  if (key_valid != nullptr || key_bias != nullptr) {
+    const int64_t need = ((int64_t)Sk + 3) / 4 * 4;
+    if (key_mask_stride < need || key_mask_stride % 4 != 0)
+      return fail(VX_ERR_INVALID_ARGUMENT,
+                  "key_mask_stride (%lld) must be a multiple of 4 and >= round_up(seq_k, 4) = %lld",
+                  (long long)key_mask_stride, (long long)need);
+    if (key_valid != nullptr && (reinterpret_cast<uintptr_t>(key_valid) & 3u) != 0)
+      return fail(VX_ERR_INVALID_ARGUMENT, "key_valid must be 4-byte aligned");
+    if (key_bias != nullptr && !aligned16(key_bias))
+      return fail(VX_ERR_INVALID_ARGUMENT, "key_bias must be 16-byte aligned");
+  }
+  int64_t qs[3], ks[3], vs[3], os[3];
+  strides_or_default(qs_in, Sq, H, D, qs);
+  strides_or_default(ks_in, Sk, H, D, ks);
+  strides_or_default(vs_in, Sk, H, D, vs);
+  strides_or_default(os_in, Sq, H, D, os);
+  int32_t rc;
+  if ((rc = check_strides("q", qs, Sq)) != VX_OK) return rc;
+  if ((rc = check_strides("k", ks, Sk)) != VX_OK) return rc;
+  if ((rc = check_strides("v", vs, Sk)) != VX_OK) return rc;
+  if ((rc = check_strides("out", os, Sq)) != VX_OK) return rc;
+  if (args != nullptr) {
+    args->q = q;
+    args->k = k;
+    args->v = v;
+    args->o = const_cast<void*>(out);
+    args->kv_len = kv_len;
+    args->key_valid = key_valid;
+    args->key_bias = key_bias;
+    args->key_mask_stride = key_mask_stride;
+    args->B = B;
+    args->Sq = Sq;
+    args->Sk = Sk;
+    args->H = H;
+    args->D = D;
+    for (int i = 0; i < 3; ++i) {
+      args->qs[i] = qs[i];
+      args->ks[i] = ks[i];
+      args->vs[i] = vs[i];
+      args->os[i] = os[i];
+    }
+    args->scale = scale;
+  }
+  return ok();
+}
+
+int32_t na3d_check(const void* q, const void* k, const void* v, const void* out, int32_t B, int32_t T, int32_t Hs,
+                   int32_t W, int32_t NH, int32_t D, int32_t kt, int32_t kh, int32_t kw, float scale,
+                   vx::Na3dArgs* args) {
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr)
+    return fail(VX_ERR_INVALID_ARGUMENT, "q, k, v and out must be non-NULL");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(VX_ERR_INVALID_ARGUMENT, "q, k, v and out must be 16-byte aligned");
+  if (B < 1 || T < 1 || Hs < 1 || W < 1 || NH < 1)
+    return fail(VX_ERR_INVALID_ARGUMENT, "batch (%d), t (%d), h (%d), w (%d) and num_heads (%d) must be >= 1", B, T, Hs,
+                W, NH);
+  if (kt < 1 || kh < 1 || kw < 1)
+    return fail(VX_ERR_INVALID_ARGUMENT, "kernel sizes must be >= 1 (got %d, %d, %d)", kt, kh, kw);
+  if (D != 128 && D != 64) return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (64 or 128)", D);
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(VX_ERR_INVALID_ARGUMENT, "scale must be positive and finite (got %g)", (double)scale);
+  const int64_t tokens = (int64_t)T * Hs * W;
+  if (tokens * NH * D > ((int64_t)1 << 40))
+    return fail(VX_ERR_INVALID_ARGUMENT, "tensor of %lld elements per batch item is too large",
+                (long long)(tokens * NH * D));
+  if ((int64_t)T * Hs * W > 0x7fffffff) return fail(VX_ERR_INVALID_ARGUMENT, "grid too large");
+  if (args != nullptr) {
+    args->q = q;
+    args->k = k;
+    args->v = v;
+    args->o = const_cast<void*>(out);
+    args->B = B;
+    args->T = T;
+    args->Hs = Hs;
+    args->W = W;
+    args->NH = NH;
+    args->D = D;
+    args->kt = kt < T ? kt : T;
+    args->kh = kh < Hs ? kh : Hs;
+    args->kw = kw < W ? kw : W;
+    args->scale = scale;
+  }
+  return ok();
+}
+
+int32_t injected() {
+  const int32_t code = g_inject.load(std::memory_order_relaxed);
+  if (code != 0) return fail(code, "error injected by vx_debug_inject_error(%d)", code);
+  return VX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t vx_abi_version(void) { return 10000; }
+
+const char* vx_last_error(void) { return g_error; }
+
+void vx_debug_inject_error(int32_t code) { g_inject.store(code, std::memory_order_relaxed); }
+
+int32_t vx_flash_attn_check(const void* q, const void* k, const void* v, const void* out, const int32_t* kv_len,
+                            const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride,
+                            int32_t batch, int32_t seq_q,
+                            int32_t seq_k, int32_t num_heads, int32_t head_dim, const int64_t* q_strides,
+                            const int64_t* k_strides, const int64_t* v_strides, const int64_t* out_strides,
+                            float scale) {
+  return flash_check(q, k, v, out, kv_len, key_valid, key_bias, key_mask_stride, batch, seq_q, seq_k, num_heads,
+                     head_dim,
+                     q_strides, k_strides, v_strides, out_strides, scale, nullptr);
+}
+
+int32_t vx_flash_attn_fwd(const void* q, const void* k, const void* v, void* out, const int32_t* kv_len,
+                          const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride,
+                          int32_t batch, int32_t seq_q,
+                          int32_t seq_k, int32_t num_heads, int32_t head_dim, const int64_t* q_strides,
+                          const int64_t* k_strides, const int64_t* v_strides, const int64_t* out_strides, float scale,
+                          void* stream) {
+  vx::FlashArgs args;
+  int32_t rc = flash_check(q, k, v, out, kv_len, key_valid, key_bias, key_mask_stride, batch, seq_q, seq_k,
+                           num_heads, head_dim, q_strides, k_strides, v_strides, out_strides, scale, &args);
+  if (rc != VX_OK) return rc;
+  if ((rc = injected()) != VX_OK) return rc;
+  const int err = vx::launch_flash_fwd(args, stream);
+  if (err != 0) return fail(VX_ERR_LAUNCH, "flash attention launch failed (hipError_t %d)", err);
+  return ok();
+}
+
+int32_t vx_na3d_check(const void* q, const void* k, const void* v, const void* out, int32_t batch, int32_t t,
+                      int32_t h, int32_t w, int32_t num_heads, int32_t head_dim, int32_t kernel_t, int32_t kernel_h,
+                      int32_t kernel_w, float scale) {
+  return na3d_check(q, k, v, out, batch, t, h, w, num_heads, head_dim, kernel_t, kernel_h, kernel_w, scale, nullptr);
+}
+
+int32_t vx_na3d_fwd(const void* q, const void* k, const void* v, void* out, int32_t batch, int32_t t, int32_t h,
+                    int32_t w, int32_t num_heads, int32_t head_dim, int32_t kernel_t, int32_t kernel_h,
+                    int32_t kernel_w, float scale, void* stream) {
+  vx::Na3dArgs args;
+  int32_t rc = na3d_check(q, k, v, out, batch, t, h, w, num_heads, head_dim, kernel_t, kernel_h, kernel_w, scale,
+                          &args);
+  if (rc != VX_OK) return rc;
+  if ((rc = injected()) != VX_OK) return rc;
+  const int err = vx::launch_na3d_fwd(args, stream);
+  if (err != 0) return fail(VX_ERR_LAUNCH, "neighbourhood attention launch failed (hipError_t %d)", err);
+  return ok();
+}
+
+}  // extern "C"

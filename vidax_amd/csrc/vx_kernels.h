@@ -1,0 +1,42 @@
+// Internal interface between the C ABI (vx_capi.cpp, plain C++) and the HIP
+// launchers (*.hip). No HIP headers here so the argument checker builds and
+// runs on a host without a GPU.
+#pragma once
+
+#include <stdint.h>
+
+namespace vx {
+
+// Flash attention launch arguments, validated by the C ABI before use.
+// Strides are in elements: {batch, seq, head}; the head dim is contiguous.
+struct FlashArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  const int32_t* kv_len;     // [B] or nullptr
+  const uint8_t* key_valid;  // [B, key_mask_stride] or nullptr
+  const float* key_bias;     // [B, key_mask_stride] or nullptr
+  int64_t key_mask_stride;   // elements between batch rows of the key masks
+  int32_t B, Sq, Sk, H, D;
+  int64_t qs[3], ks[3], vs[3], os[3];
+  float scale;  // softmax scale (> 0)
+};
+
+// Neighbourhood attention launch arguments; tensors are contiguous
+// (B, T, Hs, W, NH, D).
+struct Na3dArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int32_t B, T, Hs, W, NH, D;
+  int32_t kt, kh, kw;  // window sizes already clamped to the grid extents
+  float scale;
+};
+
+// Both return a hipError_t value (0 on success).
+int launch_flash_fwd(const FlashArgs& a, void* stream);
+int launch_na3d_fwd(const Na3dArgs& a, void* stream);
+
+}  // namespace vx

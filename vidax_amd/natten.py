@@ -1,0 +1,56 @@
+"""3D neighbourhood attention entry point over the gfx950 HIP kernel.
+
+Mirrors `neighborhood_attention_3d(q, k, v, kernel_size)` of
+`src/vidax/models/ltx2_5/diffusion_vae.py:179-234`: (B, T, H, W, NH, HD)
+tensors, q already pre-scaled by the caller (`diffusion_vae.py:265`), NATTEN
+boundary-clamped windows (`diffusion_vae.py:152-164`), output of the same shape.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+__all__ = ["neighborhood_attention_3d", "na3d_attention"]
+
+
+def na3d_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                   kernel_size: Tuple[int, int, int], scale: float = 1.0,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Neighbourhood attention with an explicit logit scale (1.0 = reference)."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if t.dim() != 6:
+            raise ValueError(f"{name} must be (B, T, H, W, NH, HD); got {tuple(t.shape)}")
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be bfloat16; got {t.dtype}")
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be a GPU tensor")
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k and v must have the same shape")
+    if len(kernel_size) != 3:
+        raise ValueError("kernel_size must be (kt, kh, kw)")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    B, T, H, W, NH, HD = q.shape
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bf16 tensor shaped like q")
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    with torch.cuda.device(q.device):
+        rc = _lib.lib().vx_na3d_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            B, T, H, W, NH, HD, int(kernel_size[0]), int(kernel_size[1]), int(kernel_size[2]),
+            ctypes.c_float(scale), ctypes.c_void_p(stream))
+    _lib.raise_for(rc)
+    return out
+
+
+def neighborhood_attention_3d(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                              kernel_size: Tuple[int, int, int]) -> torch.Tensor:
+    """NATTEN-semantics 3D neighbourhood attention; q is pre-scaled by the caller."""
+    return na3d_attention(q, k, v, kernel_size, scale=1.0)
