@@ -171,14 +171,16 @@ def attention_rows(q, k, v, rows, scale=None, kv_len=None, key_valid=None, key_b
 
 # ------------------------------------------------- neighbourhood attention
 def na3d(q, k, v, kernel_size, scale=1.0, acc=np.float64, round_logits_bf16=False,
-         round_weights_bf16=False):
+         round_weights_bf16=False, ty_rows=None):
     """3D neighbourhood attention over (B, T, H, W, NH, D) tensors.
 
     Window gather per axis (`window_indices`), then per query a softmax over
     its kt'*kh'*kw' keys. `scale` multiplies the logits (the reference's
     caller pre-scales q and passes no scale, i.e. 1.0). The optional rounding
     flags reproduce the reference's dtype points (bf16 logits, bf16 weights;
-    `diffusion_vae.py:222-223`).
+    `diffusion_vae.py:222-223`). `ty_rows`, a list of (t, y) query rows,
+    restricts the computation to those rows (others are left at zero); each
+    output row depends only on its own queries, so the subset is exact.
     """
     q = np.asarray(q)
     k = np.asarray(k)
@@ -189,24 +191,24 @@ def na3d(q, k, v, kernel_size, scale=1.0, acc=np.float64, round_logits_bf16=Fals
     ih = window_indices(Hs, kh)  # (Hs, kh')
     iw = window_indices(W, kw)   # (W, kw')
     out = np.zeros(q.shape, dtype=acc)
+    rows = [(t, y) for t in range(T) for y in range(Hs)] if ty_rows is None else list(ty_rows)
     for b in range(B):
-        for t in range(T):
-            for y in range(Hs):
-                qq = q[b, t, y].astype(acc)                      # (W, NH, D)
-                # keys: (kt', kh', W, kw', NH, D)
-                kk = k[b][np.ix_(it[t], ih[y])]                   # (kt', kh', W, NH, D)
-                vv = v[b][np.ix_(it[t], ih[y])]
-                kk = kk[:, :, iw]                                 # (kt', kh', W, kw', NH, D)
-                vv = vv[:, :, iw]
-                kk = np.moveaxis(kk, 2, 0).reshape(W, -1, NH, D).astype(acc)
-                vv = np.moveaxis(vv, 2, 0).reshape(W, -1, NH, D).astype(acc)
-                logits = np.einsum("wnd,wknd->wnk", qq, kk) * acc(scale)
-                if round_logits_bf16:
-                    logits = bf16_round(logits.astype(np.float32)).astype(acc)
-                w = _softmax_rows(logits)
-                if round_weights_bf16:
-                    w = bf16_round(w.astype(np.float32)).astype(acc)
-                out[b, t, y] = np.einsum("wnk,wknd->wnd", w, vv)
+        for t, y in rows:
+            qq = q[b, t, y].astype(acc)                      # (W, NH, D)
+            # keys: (kt', kh', W, kw', NH, D)
+            kk = k[b][np.ix_(it[t], ih[y])]                   # (kt', kh', W, NH, D)
+            vv = v[b][np.ix_(it[t], ih[y])]
+            kk = kk[:, :, iw]                                 # (kt', kh', W, kw', NH, D)
+            vv = vv[:, :, iw]
+            kk = np.moveaxis(kk, 2, 0).reshape(W, -1, NH, D).astype(acc)
+            vv = np.moveaxis(vv, 2, 0).reshape(W, -1, NH, D).astype(acc)
+            logits = np.einsum("wnd,wknd->wnk", qq, kk) * acc(scale)
+            if round_logits_bf16:
+                logits = bf16_round(logits.astype(np.float32)).astype(acc)
+            w = _softmax_rows(logits)
+            if round_weights_bf16:
+                w = bf16_round(w.astype(np.float32)).astype(acc)
+            out[b, t, y] = np.einsum("wnk,wknd->wnd", w, vv)
     return out
 
 

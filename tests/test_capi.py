@@ -1,0 +1,156 @@
+"""CPU tests of the C ABI: the library loads without a GPU, exports every
+symbol include/vx_attn.h declares, and its argument checks, error codes,
+messages and failure injection behave as documented. No kernel is launched:
+every call here is rejected (or short-circuited by the injection hook) on the
+host before any HIP call."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from vidax_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "vx_attn.h")
+
+A = 1 << 20  # a 16-byte aligned fake device address (never dereferenced)
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vx_\w+)\s*\(", text)))
+
+
+def test_header_symbols_are_exported():
+    L = _lib.lib()
+    names = _declared()
+    assert set(names) == set(_lib.EXPORTED_SYMBOLS)
+    for n in names:
+        assert hasattr(L, n), n
+
+
+def test_abi_version():
+    assert _lib.lib().vx_abi_version() == 10000
+
+
+def _flash_check(**kw):
+    args = dict(q=A, k=A, v=A, out=A, kv_len=None, key_valid=None, key_bias=None, stride=0,
+                B=1, Sq=100, Sk=200, H=4, D=128, qs=None, ks=None, vs=None, os_=None, scale=0.088)
+    args.update(kw)
+    s3 = lambda s: None if s is None else _lib.strides3(s)
+    return _lib.lib().vx_flash_attn_check(
+        args["q"], args["k"], args["v"], args["out"], args["kv_len"], args["key_valid"],
+        args["key_bias"], args["stride"], args["B"], args["Sq"], args["Sk"], args["H"], args["D"],
+        s3(args["qs"]), s3(args["ks"]), s3(args["vs"]), s3(args["os_"]), ctypes.c_float(args["scale"]))
+
+
+def test_flash_check_accepts_valid_arguments():
+    assert _flash_check() == _lib.VX_OK
+    assert _lib.last_error() == ""
+    assert _flash_check(qs=(200 * 4 * 128, 4 * 128, 128)) == _lib.VX_OK
+    assert _flash_check(key_valid=A, stride=200) == _lib.VX_OK
+    assert _flash_check(key_bias=A, kv_len=A, stride=204) == _lib.VX_OK
+
+
+@pytest.mark.parametrize("kw,code,frag", [
+    (dict(q=None), _lib.VX_ERR_INVALID_ARGUMENT, "non-NULL"),
+    (dict(out=A + 8), _lib.VX_ERR_INVALID_ARGUMENT, "aligned"),
+    (dict(B=0), _lib.VX_ERR_INVALID_ARGUMENT, ">= 1"),
+    (dict(Sk=0), _lib.VX_ERR_INVALID_ARGUMENT, ">= 1"),
+    (dict(H=70000), _lib.VX_ERR_INVALID_ARGUMENT, "65535"),
+    (dict(D=64), _lib.VX_ERR_UNSUPPORTED, "head_dim"),
+    (dict(scale=0.0), _lib.VX_ERR_INVALID_ARGUMENT, "scale"),
+    (dict(scale=float("inf")), _lib.VX_ERR_INVALID_ARGUMENT, "scale"),
+    (dict(scale=-1.0), _lib.VX_ERR_INVALID_ARGUMENT, "scale"),
+    (dict(qs=(0, 4 * 128, 129)), _lib.VX_ERR_INVALID_ARGUMENT, "multiple of 8"),
+    (dict(ks=(0, -512, 128)), _lib.VX_ERR_INVALID_ARGUMENT, "negative"),
+    (dict(key_valid=A, stride=199), _lib.VX_ERR_INVALID_ARGUMENT, "key_mask_stride"),
+    (dict(key_valid=A, stride=198), _lib.VX_ERR_INVALID_ARGUMENT, "key_mask_stride"),
+    (dict(key_valid=A + 2, stride=200), _lib.VX_ERR_INVALID_ARGUMENT, "4-byte"),
+    (dict(key_bias=A + 4, stride=200), _lib.VX_ERR_INVALID_ARGUMENT, "16-byte"),
+])
+def test_flash_check_rejects(kw, code, frag):
+    assert _flash_check(**kw) == code
+    assert frag in _lib.last_error()
+
+
+def _na_check(**kw):
+    args = dict(q=A, k=A, v=A, out=A, B=1, T=4, H=6, W=9, NH=2, D=128, kt=3, kh=5, kw=5, scale=1.0)
+    args.update(kw)
+    return _lib.lib().vx_na3d_check(args["q"], args["k"], args["v"], args["out"], args["B"], args["T"],
+                                    args["H"], args["W"], args["NH"], args["D"], args["kt"], args["kh"],
+                                    args["kw"], ctypes.c_float(args["scale"]))
+
+
+def test_na3d_check():
+    assert _na_check() == _lib.VX_OK
+    assert _na_check(kt=100, kh=100, kw=100) == _lib.VX_OK          # clamped to the grid
+    assert _na_check(W=200, kw=57) == _lib.VX_OK
+    assert _na_check(W=200, kw=58) == _lib.VX_ERR_UNSUPPORTED
+    assert _na_check(kt=0) == _lib.VX_ERR_INVALID_ARGUMENT
+    assert _na_check(D=64) == _lib.VX_ERR_UNSUPPORTED
+    assert _na_check(T=0) == _lib.VX_ERR_INVALID_ARGUMENT
+    assert _na_check(k=A + 1) == _lib.VX_ERR_INVALID_ARGUMENT
+    assert _na_check(scale=float("nan")) == _lib.VX_ERR_INVALID_ARGUMENT
+
+
+def test_fwd_rejects_before_launch():
+    """Invalid arguments fail in the checker: no HIP call, so this runs without a GPU."""
+    L = _lib.lib()
+    rc = L.vx_flash_attn_fwd(A, A, A, A, None, None, None, 0, 1, 10, 10, 1, 96, None, None, None, None,
+                             ctypes.c_float(1.0), None)
+    assert rc == _lib.VX_ERR_UNSUPPORTED and "head_dim" in _lib.last_error()
+    rc = L.vx_na3d_fwd(A, A, A, A, 1, 0, 1, 1, 1, 128, 1, 1, 1, ctypes.c_float(1.0), None)
+    assert rc == _lib.VX_ERR_INVALID_ARGUMENT
+
+
+def test_error_injection_short_circuits_launch():
+    """The failure-injection hook returns its code after the argument checks
+    and before any launch, so the error path can be exercised on a CPU host."""
+    L = _lib.lib()
+    L.vx_debug_inject_error(_lib.VX_ERR_LAUNCH)
+    try:
+        rc = L.vx_flash_attn_fwd(A, A, A, A, None, None, None, 0, 1, 10, 10, 1, 128, None, None, None, None,
+                                 ctypes.c_float(1.0), None)
+        assert rc == _lib.VX_ERR_LAUNCH and "injected" in _lib.last_error()
+        with pytest.raises(_lib.VxError):
+            _lib.raise_for(rc)
+        rc = L.vx_na3d_fwd(A, A, A, A, 1, 2, 2, 2, 1, 128, 1, 1, 1, ctypes.c_float(1.0), None)
+        assert rc == _lib.VX_ERR_LAUNCH
+    finally:
+        L.vx_debug_inject_error(0)
+    # invalid arguments still win over the injection
+    L.vx_debug_inject_error(_lib.VX_ERR_LAUNCH)
+    try:
+        rc = L.vx_flash_attn_fwd(None, A, A, A, None, None, None, 0, 1, 10, 10, 1, 128, None, None, None, None,
+                                 ctypes.c_float(1.0), None)
+        assert rc == _lib.VX_ERR_INVALID_ARGUMENT
+    finally:
+        L.vx_debug_inject_error(0)
+
+
+def test_error_message_is_thread_local():
+    import threading
+    L = _lib.lib()
+    assert _flash_check(D=64) == _lib.VX_ERR_UNSUPPORTED
+    seen = {}
+
+    def other():
+        seen["msg"] = _lib.last_error()
+    th = threading.Thread(target=other)
+    th.start()
+    th.join()
+    assert seen["msg"] == ""
+    assert "head_dim" in _lib.last_error()
+
+
+def test_raise_for_maps_codes():
+    _lib.raise_for(_lib.VX_OK)
+    _flash_check(D=64)
+    with pytest.raises(NotImplementedError):
+        _lib.raise_for(_lib.VX_ERR_UNSUPPORTED)
+    _flash_check(B=0)
+    with pytest.raises(ValueError):
+        _lib.raise_for(_lib.VX_ERR_INVALID_ARGUMENT)

@@ -1,0 +1,112 @@
+"""GPU parity tests of the 3D neighbourhood-attention kernel against the oracle.
+
+Same bar as the flash kernel: max-abs <= 2e-2, mean-abs <= 2e-3, plus a
+mean-abs / RMS bound. q is pre-scaled (the reference's caller convention) and
+the kernel is called with scale 1.0 through `neighborhood_attention_3d`.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_ABS = 2e-3
+MEAN_REL_RMS = 1e-2
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _t(x, dev):
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(dev).to(torch.bfloat16)
+
+
+def _check(o, ref, label):
+    d = np.abs(o.astype(np.float64) - ref)
+    rms = float(np.sqrt(np.mean(ref ** 2))) + 1e-30
+    mx, mean = float(d.max()), float(d.mean())
+    print(f"  {label}: max_abs={mx:.3e} mean_abs={mean:.3e} mean/rms={mean / rms:.3e}", flush=True)
+    assert np.isfinite(o).all(), f"{label}: non-finite output"
+    assert mx <= MAX_ABS and mean <= MEAN_ABS and mean / rms <= MEAN_REL_RMS, label
+
+
+NA_CASES = [
+    # (B, T, H, W, NH), kernel, seed
+    ((1, 3, 8, 16, 2), (3, 7, 7), 30),     # exact bricks
+    ((1, 4, 6, 9, 2), (3, 5, 5), 31),      # ragged bricks (H % 4, W % 8)
+    ((2, 2, 5, 7, 1), (3, 3, 3), 32),      # kt clamped to T
+    ((1, 5, 13, 21, 3), (3, 7, 7), 33),
+    ((1, 3, 9, 11, 1), (2, 4, 6), 34),     # even windows
+    ((1, 2, 3, 4, 2), (5, 9, 9), 35),      # every window clamped: full attention
+    ((1, 3, 4, 30, 1), (1, 1, 25), 36),    # wide x window (two 16-key segments)
+    ((1, 2, 4, 70, 1), (1, 3, 57), 37),    # widest supported x window
+]
+
+
+@pytest.mark.parametrize("shape,ks,seed", NA_CASES)
+def test_na3d_small(gpu, shape, ks, seed):
+    from vidax_amd import neighborhood_attention_3d
+    B, T, H, W, NH = shape
+    _say(f"na3d shape={shape} kernel={ks} seed={seed}")
+    q, k, v = O.make_na3d_inputs(B, T, H, W, NH, 128, seed)
+    out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), ks)
+    torch.cuda.synchronize()
+    _check(out.float().cpu().numpy(), O.na3d(q, k, v, ks), "oracle")
+
+
+def test_na3d_window_one_is_identity(gpu):
+    from vidax_amd import neighborhood_attention_3d
+    _say("na3d window (1,1,1) identity")
+    q, k, v = O.make_na3d_inputs(1, 3, 7, 10, 2, 128, 38)
+    out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), (1, 1, 1))
+    np.testing.assert_array_equal(out.float().cpu().numpy(), v)
+
+
+def test_na3d_full_window_equals_flash(gpu):
+    """A window covering the grid is full attention over the T*H*W tokens:
+    the NA kernel must agree with the flash kernel on the flattened tokens."""
+    from vidax_amd import flash_attention, neighborhood_attention_3d
+    _say("na3d full window vs flash")
+    B, T, H, W, NH = 1, 2, 4, 6, 2
+    q, k, v = O.make_na3d_inputs(B, T, H, W, NH, 128, 39)
+    tq, tk, tv = _t(q, gpu), _t(k, gpu), _t(v, gpu)
+    out = neighborhood_attention_3d(tq, tk, tv, (T, H, W))
+    flat = lambda x: x.reshape(B, T * H * W, NH, 128)
+    ref = flash_attention(flat(tq), flat(tk), flat(tv), scale=1.0).reshape(out.shape)
+    d = (out.float() - ref.float()).abs()
+    assert d.max().item() <= 1e-2 and d.mean().item() <= 1e-3
+
+
+def test_na3d_deterministic(gpu):
+    from vidax_amd import neighborhood_attention_3d
+    _say("na3d determinism")
+    q, k, v = O.make_na3d_inputs(1, 3, 9, 17, 2, 128, 40)
+    tq, tk, tv = _t(q, gpu), _t(k, gpu), _t(v, gpu)
+    a = neighborhood_attention_3d(tq, tk, tv, (3, 7, 7))
+    b = neighborhood_attention_3d(tq, tk, tv, (3, 7, 7))
+    assert torch.equal(a, b)
+
+
+@pytest.mark.slow
+def test_na3d_config4_sampled_rows(gpu):
+    """Config shape: grid 21x45x80, window (3,7,7), B=1 NH=24 D=128; every
+    query of 14 sampled (t, y) rows (borders included) against the oracle."""
+    from vidax_amd import neighborhood_attention_3d
+    _say("na3d c4 21x45x80 NH=24 (3,7,7) sampled rows")
+    B, T, H, W, NH = 1, 21, 45, 80, 24
+    q, k, v = O.make_na3d_inputs(B, T, H, W, NH, 128, 3)
+    out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), (3, 7, 7))
+    o = out.float().cpu().numpy()
+    rows = [(0, 0), (0, 44), (20, 0), (20, 44), (1, 1), (10, 22), (10, 3), (19, 43),
+            (5, 40), (15, 2), (2, 21), (18, 30), (11, 44), (9, 0)]
+    ref = O.na3d(q, k, v, (3, 7, 7), ty_rows=rows)
+    sel = tuple(np.array(rows).T)
+    _check(o[0][sel], ref[0][sel], "c4 rows")
+    # the reference's own dtype points (bf16 logits and weights) stay within the bar too
+    ref_bf = O.na3d(q, k, v, (3, 7, 7), ty_rows=rows[:4], round_logits_bf16=True, round_weights_bf16=True)
+    sel4 = tuple(np.array(rows[:4]).T)
+    _check(o[0][sel4], ref_bf[0][sel4], "c4 rows vs bf16-logit reference")
