@@ -1,23 +1,28 @@
 // Non-causal flash attention forward for gfx950, bf16 in/out, D = 128.
 //
-// Work decomposition: one workgroup per (query tile, head, batch); WAVES
-// waves per workgroup, each owning NQB blocks of 32 query rows. The wave
+// Work decomposition: one workgroup of 8 waves per (256-query tile, head,
+// batch item); each wave owns 32 query rows, two waves per SIMD. The wave
 // computes S^T = K Q^T so that every lane owns one query column of the MFMA
 // output: row max, row sum and the output rescale are per-lane scalars and the
 // two halves of the wave are combined with one v_permlane32_swap. Q stays in
 // registers as the B operand for the whole key loop. K and V tiles of 64 keys
-// are staged through registers into double-buffered, XOR-swizzled LDS; K is
-// read back with ds_read_b128 (A operand of QK^T) and V with the gfx950
-// transpose read ds_read_b64_tr_b16 (A operand of O^T = V^T P^T). The QK^T of
-// tile t+1 is issued before the softmax of tile t so the matrix cores and
-// the VALU overlap within a wave.
+// are staged through registers into XOR-swizzled LDS (K double-, V triple-
+// buffered); K is read back with ds_read_b128 (A operand of QK^T) and V with
+// the gfx950 transpose read ds_read_b64_tr_b16 (A operand of O^T = V^T P^T).
 //
-// Softmax: scores are kept in log2 units (scale * log2(e) folded into one
-// FMA before v_exp_f32). The running row max is only raised when a tile's
-// max exceeds it by more than kRescaleSlack (log2 units), which bounds the
-// unnormalised probabilities by 2^kRescaleSlack and makes the O rescale rare;
-// the final division by the row sum makes the result independent of the
-// reference point.
+// Software pipeline: iteration t issues the MFMAs of QK^T(t+1) and of
+// PV(t-1) in one branch-free block together with the softmax VALU work of
+// tile t, interleaved slot by slot (one MFMA, the LDS read two slots ahead and
+// one score's exp per slot, fenced with sched_barrier), so the matrix cores and
+// the VALU of a wave run concurrently.
+//
+// Softmax: scores are kept in log2 units (scale * log2(e) folded into the FMA
+// that feeds v_exp_f32). The running row max is only raised when a tile's max
+// exceeds it by more than kRescaleSlack (log2 units): the probabilities are
+// computed speculatively against the current max and recomputed in the rare
+// case that a rescale is needed, which bounds the unnormalised probabilities
+// by 2^kRescaleSlack. The final division by the row sum makes the result
+// independent of the reference point.
 #include "vx_gfx950.hpp"
 #include "vx_kernels.h"
 
@@ -26,8 +31,15 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kBN = 64;                       // keys per tile
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kQueriesPerBlock = kWaves * 32;
 constexpr int kRowBytes = kD * 2;             // one bf16 key row
 constexpr int kTileBytes = kBN * kRowBytes;   // 16 KiB
+constexpr int kKBuf = 0;                      // two K tiles
+constexpr int kVBuf = 2 * kTileBytes;         // three V tiles
+constexpr int kSmemBytes = 5 * kTileBytes;    // 80 KiB
+constexpr int kLoadsPerWave = (kBN / 4) / kWaves;  // 1 KiB wave loads per tile
 constexpr float kRescaleSlack = 8.0f;         // log2 units
 constexpr float kNegBig = -1.0e30f;           // finite "no key seen yet" max
 
@@ -37,32 +49,24 @@ constexpr float kNegBig = -1.0e30f;           // finite "no key seen yet" max
 // pairs (the transpose reads of V).
 __device__ __forceinline__ int row_swizzle(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
-template <int NQB, int WAVES, bool MASKED>
-struct FlashTile {
-  static constexpr int kThreads = WAVES * 64;
-  static constexpr int kQueriesPerWave = NQB * 32;
-  static constexpr int kQueriesPerBlock = WAVES * kQueriesPerWave;
-  static constexpr int kLoadsPerWave = (kBN / 4) / WAVES;  // 1 KiB wave loads per tile
-  static_assert(kLoadsPerWave >= 1, "too many waves for one tile");
-};
+typedef VX_LDS unsigned char lds_u8;
 
-template <int NQB, int WAVES, bool MASKED>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVES / 4, WAVES / 4)))
+// NaN test on the bit pattern (stays exact when the compiler may assume no NaNs).
+__device__ __forceinline__ bool is_nan_bits(float x) { return (__float_as_uint(x) & 0x7fffffffu) > 0x7f800000u; }
+
+template <bool MASKED>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_fwd_kernel(const FlashArgs a) {
-  using T = FlashTile<NQB, WAVES, MASKED>;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[4 * kTileBytes];
-  unsigned char* const kbuf0 = smem;
-  unsigned char* const kbuf1 = smem + kTileBytes;
-  unsigned char* const vbuf0 = smem + 2 * kTileBytes;
-  unsigned char* const vbuf1 = smem + 3 * kTileBytes;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kSmemBytes];
+  lds_u8* const lds = (lds_u8*)smem;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int hf = lane >> 5;   // which half of the wave
-  const int col = lane & 31;  // query column within a 32-block
+  const int col = lane & 31;  // query column within the wave's 32
   const int b = blockIdx.z;
   const int head = blockIdx.y;
-  const int qw0 = (blockIdx.x * WAVES + wave) * T::kQueriesPerWave;
+  const int qw0 = (blockIdx.x * kWaves + wave) * 32;
 
   const bf16* qg = (const bf16*)a.q + b * a.qs[0] + head * a.qs[2];
   const bf16* kg = (const bf16*)a.k + b * a.ks[0] + head * a.ks[2];
@@ -75,17 +79,16 @@ void flash_fwd_kernel(const FlashArgs a) {
   const float c = a.scale * kLog2e;
 
   // ---- Q (B operand of S^T = K Q^T), resident for the whole key loop.
-  bf16x8 qr[NQB][8];
-#pragma unroll
-  for (int qb = 0; qb < NQB; ++qb) {
-    const int qi = min(qw0 + qb * 32 + col, a.Sq - 1);
+  bf16x8 qr[8];
+  {
+    const int qi = min(qw0 + col, a.Sq - 1);
     const bf16* p = qg + (int64_t)qi * a.qs[1] + hf * 8;
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) qr[qb][ds] = *(const bf16x8*)(p + ds * 16);
+    for (int ds = 0; ds < 8; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
   }
 
-  // ---- per-lane LDS offsets.
-  // K fragment (kb, ds): row kb*32 + col, chunk 2*ds + hf, swizzled by row%8 = col%8.
+  // ---- per-lane LDS byte offsets inside one tile.
+  // K fragment (kb, ds): row kb*32 + col, chunk 2*ds + hf, swizzled by col%8.
   const int ksw = row_swizzle(col);
   int koff[4];
 #pragma unroll
@@ -99,81 +102,111 @@ void flash_fwd_kernel(const FlashArgs a) {
 #pragma unroll
   for (int db1 = 0; db1 < 2; ++db1)
     voff[db1] = (hf * 4 + vr) * kRowBytes + (((4 * db1 + 2 * dh + (vc >> 1)) ^ vsw) * 16) + (vc & 1) * 8;
+  // staging: this lane's row within its 4-row group and its 16-byte column
+  const int srow = lane >> 4;
+  const int scol = lane & 15;
 
   // ---- global -> register -> LDS staging of one 64-key tile.
-  u32x4 kst[T::kLoadsPerWave], vst[T::kLoadsPerWave];
   auto gload = [&](const bf16* base, int64_t sstride, int t, u32x4* st) {
 #pragma unroll
-    for (int p = 0; p < T::kLoadsPerWave; ++p) {
-      const int r = (wave * T::kLoadsPerWave + p) * 4 + (lane >> 4);
+    for (int p = 0; p < kLoadsPerWave; ++p) {
+      const int r = (wave * kLoadsPerWave + p) * 4 + srow;
       const int key = min(t * kBN + r, kv_end - 1);
-      st[p] = *(const u32x4*)(base + (int64_t)key * sstride + (lane & 15) * 8);
+      st[p] = *(const u32x4*)(base + (int64_t)key * sstride + scol * 8);
     }
   };
-  auto lstore = [&](unsigned char* buf, const u32x4* st) {
+  auto lstore = [&](int buf_off, const u32x4* st) {
 #pragma unroll
-    for (int p = 0; p < T::kLoadsPerWave; ++p) {
-      const int r = (wave * T::kLoadsPerWave + p) * 4 + (lane >> 4);
-      const int pos = (lane & 15) ^ row_swizzle(r);
-      *(u32x4*)(buf + r * kRowBytes + pos * 16) = st[p];
+    for (int p = 0; p < kLoadsPerWave; ++p) {
+      const int r = (wave * kLoadsPerWave + p) * 4 + srow;
+      *(VX_LDS u32x4*)(lds + buf_off + r * kRowBytes + ((scol ^ row_swizzle(r)) * 16)) = st[p];
     }
   };
 
-  auto qk = [&](const unsigned char* buf, f32x16 (&S)[2][NQB]) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) S[kb][qb] = f32x16{};
+  auto qk = [&](int buf_off, f32x16 (&S)[2]) {
+    S[0] = f32x16{};
+    S[1] = f32x16{};
+    const lds_u8* kb0 = lds + buf_off;
 #pragma unroll
     for (int ds = 0; ds < 8; ++ds) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 kf =
-            *(const bf16x8*)(buf + kb * 32 * kRowBytes + (ds >> 2) * 128 + koff[ds & 3]);
-#pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) S[kb][qb] = mfma32x32x16(kf, qr[qb][ds], S[kb][qb]);
+        const bf16x8 kf = *(const VX_LDS bf16x8*)(kb0 + koff[ds & 3] + kb * 32 * kRowBytes + (ds >> 2) * 128);
+        S[kb] = mfma32x32x16(kf, qr[ds], S[kb]);
       }
     }
   };
+  auto pv = [&](int buf_off, const bf16x8 (&P)[2][2], f32x16 (&O)[4]) {
+    const lds_u8* vb = lds + buf_off;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const lds_u8* p = vb + voff[db & 1] + (kb * 32 + 16 * j) * kRowBytes + (db >> 1) * 128;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p);
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + 8 * kRowBytes));
+          const bf16x8 vf = concat(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi));
+          O[db] = mfma32x32x16(vf, P[kb][j], O[db]);
+        }
+  };
+  // exp2 of the (speculative) probabilities of one tile, their bf16 packing
+  // and their sum.
+  auto probs = [&](const f32x16 (&S)[2], float cc, float m, bf16x8 (&P)[2][2]) -> float {
+    const float mneg = -m;
+    float l = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        bf16x8 pv8;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) pv8[r] = (bf16)fast_exp2(__builtin_fmaf(S[kb][8 * j + r], cc, mneg));
+        P[kb][j] = pv8;
+        l = sum8(pv8, l);
+      }
+    return l;
+  };
 
-  f32x16 O[4][NQB];
+  f32x16 O[4];
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) O[db][qb] = f32x16{};
-  float m_run[NQB], l_run[NQB];
-#pragma unroll
-  for (int qb = 0; qb < NQB; ++qb) {
-    m_run[qb] = kNegBig;
-    l_run[qb] = 0.f;
-  }
+  for (int db = 0; db < 4; ++db) O[db] = f32x16{};
+  float m_run = kNegBig, l_run = 0.f;
 
   const uint8_t* vrow = (MASKED && a.key_valid) ? a.key_valid + (int64_t)b * a.key_mask_stride : nullptr;
   const float* brow = (MASKED && a.key_bias) ? a.key_bias + (int64_t)b * a.key_mask_stride : nullptr;
 
   if (n_tiles > 0) {
-    // Prologue: K0, V0 and K1 into LDS, then S(0).
+    u32x4 kst[kLoadsPerWave], vst[kLoadsPerWave];
+    // Prologue: K0 -> K buffer 0, V0 -> V buffer 0, K1 -> K buffer 1 and a
+    // zeroed V buffer 2 that stands in for "V_{-1}" (paired with P = 0).
     gload(kg, a.ks[1], 0, kst);
     gload(vg, a.vs[1], 0, vst);
-    lstore(kbuf0, kst);
-    lstore(vbuf0, vst);
-    if (n_tiles > 1) {
-      gload(kg, a.ks[1], 1, kst);
-      lstore(kbuf1, kst);
-    }
+    lstore(kKBuf, kst);
+    lstore(kVBuf, vst);
+    gload(kg, a.ks[1], min(1, n_tiles - 1), kst);
+    lstore(kKBuf + kTileBytes, kst);
+#pragma unroll
+    for (int p = 0; p < kTileBytes / (kThreads * 16); ++p)
+      *(VX_LDS u32x4*)(lds + kVBuf + 2 * kTileBytes + (p * kThreads + threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
     __syncthreads();
-    f32x16 S[2][NQB];
-    qk(kbuf0, S);
+    f32x16 S[2];
+    qk(kKBuf, S);
+    bf16x8 Pp[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) Pp[kb][j] = bf16x8{};
 
+    int kb_cur = 1;   // K buffer holding K_{t+1}
+    int vb_prev = 2;  // V buffer holding V_{t-1}
     for (int t = 0; t < n_tiles; ++t) {
-      // LDS now holds K_{t+1} in kbuf[(t+1)%2] and V_t in vbuf[t%2].
+      // LDS holds K_{t+1} in K buffer kb_cur, V_{t-1} in V buffer vb_prev and
+      // V_t in V buffer (vb_prev + 1) % 3.
       __syncthreads();
-      const bool has_next = t + 1 < n_tiles;
-      if (t + 2 < n_tiles) gload(kg, a.ks[1], t + 2, kst);
-      if (has_next) gload(vg, a.vs[1], t + 1, vst);
-
-      f32x16 Sn[2][NQB];
-      if (has_next) qk((t & 1) ? kbuf0 : kbuf1, Sn);
+      gload(kg, a.ks[1], min(t + 2, n_tiles - 1), kst);
+      gload(vg, a.vs[1], min(t + 1, n_tiles - 1), vst);
 
       // ---- key masks. Tiles that hold a masked key (the tail tile, a
       // key_valid hole, any key_bias) take the scores to log2 units here,
@@ -213,107 +246,128 @@ void flash_fwd_kernel(const FlashArgs a) {
             for (int e = 0; e < 4; ++e) {
               bool ok = kbase + e < kv_end;
               if (MASKED && vrow != nullptr) ok = ok && ((vbits[kb][g] >> (8 * e)) & 0xffu) != 0;
-#pragma unroll
-              for (int qb = 0; qb < NQB; ++qb) {
-                const float sv = __builtin_fmaf(S[kb][qb][g * 4 + e], c, bias[e]);
-                S[kb][qb][g * 4 + e] = ok ? sv : -__builtin_inff();
-              }
+              const float sv = __builtin_fmaf(S[kb][g * 4 + e], c, bias[e]);
+              S[kb][g * 4 + e] = ok ? sv : -__builtin_inff();
             }
           }
         }
       }
 
-      // ---- online softmax with lazy rescale.
-      float ms[NQB];
-      bool need = false;
+      // ---- one branch-free block of 32 slots: slot s issues one MFMA
+      // (s < 16: PV(t-1) into O, s >= 16: QK^T(t+1) into Sn), the LDS read of
+      // the fragment two slots ahead, and one score's worth of softmax work for
+      // tile t (speculative against the current max). sched_barrier keeps the
+      // slots in this order so MFMA and VALU work of a wave overlap.
+      f32x16 Sn[2] = {f32x16{}, f32x16{}};
+      bf16x8 P[2][2];
+      float l_tile = 0.f;
+      float mxc = -__builtin_inff();
+      float ms = 0.f;
+      {
+        const lds_u8* kb0 = lds + kKBuf + kb_cur * kTileBytes;
+        const lds_u8* vb0 = lds + kVBuf + vb_prev * kTileBytes;
+        auto frag = [&](int s) -> bf16x8 {
+          if (s < 16) {
+            const int kb = s >> 3, j = (s >> 2) & 1, db = s & 3;
+            const lds_u8* p = vb0 + voff[db & 1] + (kb * 32 + 16 * j) * kRowBytes + (db >> 1) * 128;
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p);
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + 8 * kRowBytes));
+            return concat(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi));
+          }
+          const int ds = (s - 16) >> 1, kb = (s - 16) & 1;
+          return *(const VX_LDS bf16x8*)(kb0 + koff[ds & 3] + kb * 32 * kRowBytes + (ds >> 2) * 128);
+        };
+        const float mneg = -m_run;
+        const bf16x2 one2 = {(bf16)1.0f, (bf16)1.0f};
+        bf16x8 fr[32];
+        float pf[32];
+        bf16x2 pk[16];
+        fr[0] = frag(0);
+        fr[1] = frag(1);
 #pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) {
-        float mx = S[0][qb][0];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, S[kb][qb][i]);
-        ms[qb] = halves_max(mx) * cc;
-        need |= ms[qb] > m_run[qb] + kRescaleSlack;
-      }
-      if (__builtin_amdgcn_ballot_w64(need) != 0) {
-#pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) {
-          const float mn = fmaxf(m_run[qb], ms[qb]);
-          const float alpha = fast_exp2(m_run[qb] - mn);
-          m_run[qb] = mn;
-          l_run[qb] *= alpha;
-#pragma unroll
-          for (int db = 0; db < 4; ++db) O[db][qb] *= alpha;
+        for (int s = 0; s < 32; ++s) {
+          if (s + 2 < 32) fr[s + 2] = frag(s + 2);
+          if (s < 16) {
+            const int kb = s >> 3, j = (s >> 2) & 1, db = s & 3;
+            O[db] = mfma32x32x16(fr[s], Pp[kb][j], O[db]);
+          } else {
+            const int ds = (s - 16) >> 1, kb = (s - 16) & 1;
+            Sn[kb] = mfma32x32x16(fr[s], qr[ds], Sn[kb]);
+          }
+          pf[s] = fast_exp2(__builtin_fmaf(S[s >> 4][s & 15], cc, mneg));
+          if (s & 1) {
+            pk[s >> 1] = bf16x2{(bf16)pf[s - 1], (bf16)pf[s]};
+            l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[s >> 1], one2, l_tile, false);
+          }
+          if (s < 16) mxc = __builtin_fmaxf(__builtin_fmaxf(mxc, S[0][s]), S[1][s]);
+          if (s == 16) ms = halves_max(mxc) * cc;
+          __builtin_amdgcn_sched_barrier(0);
         }
-      }
-      bf16x8 P[2][2][NQB];
-#pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) {
-        const float mneg = -m_run[qb];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            bf16x8 pv;
-#pragma unroll
-            for (int r = 0; r < 8; ++r)
-              pv[r] = (bf16)fast_exp2(__builtin_fmaf(S[kb][qb][8 * j + r], cc, mneg));
-            P[kb][j][qb] = pv;
-            l_run[qb] = sum8(pv, l_run[qb]);
+            const int q = kb * 8 + j * 4;
+            P[kb][j] = __builtin_shufflevector(__builtin_shufflevector(pk[q], pk[q + 1], 0, 1, 2, 3),
+                                               __builtin_shufflevector(pk[q + 2], pk[q + 3], 0, 1, 2, 3),
+                                               0, 1, 2, 3, 4, 5, 6, 7);
           }
       }
 
-      // ---- O^T += V^T P^T.
-      const unsigned char* vb = (t & 1) ? vbuf1 : vbuf0;
+      // ---- rare: the tile max exceeds the reference point by more than the
+      // slack -> move it, rescale O and l, recompute this tile's probabilities.
+      // (A NaN tile sum also takes this path; testing l_tile here keeps the
+      // speculative exp work inside the block above.)
+      if (__builtin_amdgcn_ballot_w64(ms > m_run + kRescaleSlack || is_nan_bits(l_tile)) != 0) {
+        const float mn = fmaxf(m_run, ms);
+        const float alpha = fast_exp2(m_run - mn);
+        m_run = mn;
+        l_run *= alpha;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int db = 0; db < 4; ++db) {
-            const unsigned char* base = vb + (kb * 32 + 16 * j) * kRowBytes + (db >> 1) * 128 + voff[db & 1];
-            const bf16x8 vf = concat(lds_read_tr16(base), lds_read_tr16(base + 8 * kRowBytes));
-#pragma unroll
-            for (int qb = 0; qb < NQB; ++qb) O[db][qb] = mfma32x32x16(vf, P[kb][j][qb], O[db][qb]);
-          }
+        for (int db = 0; db < 4; ++db) O[db] *= alpha;
+        l_tile = probs(S, cc, m_run, P);
+      }
+      l_run += l_tile;
 
       // ---- publish the prefetched tiles (read by everyone after the next barrier).
-      if (t + 2 < n_tiles) lstore((t & 1) ? kbuf1 : kbuf0, kst);
-      if (has_next) lstore((t & 1) ? vbuf0 : vbuf1, vst);
+      const int vb_next = vb_prev == 0 ? 2 : vb_prev - 1;  // buffer of V_{t-2}, free now
+      lstore(kKBuf + (kb_cur ^ 1) * kTileBytes, kst);
+      lstore(kVBuf + vb_next * kTileBytes, vst);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb) {
+        S[kb] = Sn[kb];
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) S[kb][qb] = Sn[kb][qb];
+        for (int j = 0; j < 2; ++j) Pp[kb][j] = P[kb][j];
+      }
+      kb_cur ^= 1;
+      vb_prev = vb_prev == 2 ? 0 : vb_prev + 1;
     }
+    // ---- PV of the last tile (V_{n-1} sits in V buffer vb_prev now).
+    pv(kVBuf + vb_prev * kTileBytes, Pp, O);
   }
 
   // ---- epilogue: normalise and store (lane holds 4 consecutive d per group).
+  const float lt = halves_sum(l_run);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  const int qi = qw0 + col;
+  if (qi < a.Sq) {
+    bf16* orow = og + (int64_t)qi * a.os[1];
 #pragma unroll
-  for (int qb = 0; qb < NQB; ++qb) {
-    const float lt = halves_sum(l_run[qb]);
-    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-    const int qi = qw0 + qb * 32 + col;
-    if (qi < a.Sq) {
-      bf16* orow = og + (int64_t)qi * a.os[1];
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+      for (int g = 0; g < 4; ++g) {
+        bf16x4 ov;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          bf16x4 ov;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) ov[e] = (bf16)(O[db][qb][g * 4 + e] * inv);
-          *(bf16x4*)(orow + db * 32 + g * 8 + hf * 4) = ov;
-        }
-    }
+        for (int e = 0; e < 4; ++e) ov[e] = (bf16)(O[db][g * 4 + e] * inv);
+        *(bf16x4*)(orow + db * 32 + g * 8 + hf * 4) = ov;
+      }
   }
 }
 
-template <int NQB, int WAVES, bool MASKED>
+template <bool MASKED>
 int launch(const FlashArgs& a, hipStream_t stream) {
-  using T = FlashTile<NQB, WAVES, MASKED>;
-  dim3 grid((a.Sq + T::kQueriesPerBlock - 1) / T::kQueriesPerBlock, a.H, a.B);
-  hipLaunchKernelGGL((flash_fwd_kernel<NQB, WAVES, MASKED>), grid, dim3(T::kThreads), 0, stream, a);
+  dim3 grid((a.Sq + kQueriesPerBlock - 1) / kQueriesPerBlock, a.H, a.B);
+  hipLaunchKernelGGL((flash_fwd_kernel<MASKED>), grid, dim3(kThreads), 0, stream, a);
   return (int)hipGetLastError();
 }
 
@@ -321,8 +375,8 @@ int launch(const FlashArgs& a, hipStream_t stream) {
 
 int launch_flash_fwd(const FlashArgs& a, void* stream) {
   hipStream_t s = (hipStream_t)stream;
-  if (a.key_valid != nullptr || a.key_bias != nullptr) return launch<1, 8, true>(a, s);
-  return launch<1, 8, false>(a, s);
+  if (a.key_valid != nullptr || a.key_bias != nullptr) return launch<true>(a, s);
+  return launch<false>(a, s);
 }
 
 }  // namespace vx
