@@ -6,9 +6,11 @@
 // output: row max, row sum and the output rescale are per-lane scalars and the
 // two halves of the wave are combined with one v_permlane32_swap. Q stays in
 // registers as the B operand for the whole key loop. K and V tiles of 64 keys
-// are staged through registers into XOR-swizzled LDS (K double-, V triple-
-// buffered); K is read back with ds_read_b128 (A operand of QK^T) and V with
-// the gfx950 transpose read ds_read_b64_tr_b16 (A operand of O^T = V^T P^T).
+// are copied by the LDS DMA path (global_load_lds_dwordx4) into XOR-swizzled
+// LDS, three buffers each, two iterations ahead of their use, so their HBM /
+// L2 latency stays off the critical path; K is read back with ds_read_b128
+// (A operand of QK^T) and V with the gfx950 transpose read ds_read_b64_tr_b16
+// (A operand of O^T = V^T P^T).
 //
 // Software pipeline: iteration t issues the MFMAs of QK^T(t+1) and of
 // PV(t-1) in one branch-free block together with the softmax VALU work of
@@ -36,9 +38,9 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kQueriesPerBlock = kWaves * 32;
 constexpr int kRowBytes = kD * 2;             // one bf16 key row
 constexpr int kTileBytes = kBN * kRowBytes;   // 16 KiB
-constexpr int kKBuf = 0;                      // two K tiles
-constexpr int kVBuf = 2 * kTileBytes;         // three V tiles
-constexpr int kSmemBytes = 5 * kTileBytes;    // 80 KiB
+constexpr int kVBuf = 0;                      // three V tiles
+constexpr int kKBuf = 3 * kTileBytes;         // three K tiles
+constexpr int kSmemBytes = 6 * kTileBytes;    // 96 KiB
 constexpr int kLoadsPerWave = (kBN / 4) / kWaves;  // 1 KiB wave loads per tile
 constexpr float kRescaleSlack = 8.0f;         // log2 units
 constexpr float kNegBig = -1.0e30f;           // finite "no key seen yet" max
@@ -50,6 +52,26 @@ constexpr float kNegBig = -1.0e30f;           // finite "no key seen yet" max
 __device__ __forceinline__ int row_swizzle(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
 typedef VX_LDS unsigned char lds_u8;
+
+// One LDS DMA copy: 16 bytes per lane from `src` to LDS byte address
+// lds_row + 16 * lane (LDS base in M0). Issued as inline assembly so the
+// compiler does not treat every later LDS read as a possible reader of this
+// write (it would wait for the copy to land before the first such read); the
+// kernel orders each copy itself with wait_vmem + a barrier before any wave
+// reads the destination buffer.
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_row) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_row))
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N), other counters untouched.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
 
 // NaN test on the bit pattern (stays exact when the compiler may assume no NaNs).
 __device__ __forceinline__ bool is_nan_bits(float x) { return (__float_as_uint(x) & 0x7fffffffu) > 0x7f800000u; }
@@ -106,20 +128,19 @@ void flash_fwd_kernel(const FlashArgs a) {
   const int srow = lane >> 4;
   const int scol = lane & 15;
 
-  // ---- global -> register -> LDS staging of one 64-key tile.
-  auto gload = [&](const bf16* base, int64_t sstride, int t, u32x4* st) {
+  // ---- global -> LDS staging of one 64-key tile on the LDS DMA path
+  // (global_load_lds_dwordx4): each wave instruction fills 4 consecutive
+  // 256-byte rows, lane L landing at byte 16*L, so lane L fetches the global
+  // chunk that the swizzle places there. kLoadsPerWave instructions per tile.
+  const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+  auto stage = [&](const bf16* base, int64_t sstride, int t, int buf_off) {
 #pragma unroll
     for (int p = 0; p < kLoadsPerWave; ++p) {
-      const int r = (wave * kLoadsPerWave + p) * 4 + srow;
+      const int r0 = (wave * kLoadsPerWave + p) * 4;
+      const int r = r0 + srow;
       const int key = min(t * kBN + r, kv_end - 1);
-      st[p] = *(const u32x4*)(base + (int64_t)key * sstride + scol * 8);
-    }
-  };
-  auto lstore = [&](int buf_off, const u32x4* st) {
-#pragma unroll
-    for (int p = 0; p < kLoadsPerWave; ++p) {
-      const int r = (wave * kLoadsPerWave + p) * 4 + srow;
-      *(VX_LDS u32x4*)(lds + buf_off + r * kRowBytes + ((scol ^ row_swizzle(r)) * 16)) = st[p];
+      const bf16* src = base + (int64_t)key * sstride + ((scol ^ row_swizzle(r)) * 8);
+      lds_dma16(src, lds_base + buf_off + r0 * kRowBytes);
     }
   };
 
@@ -178,18 +199,18 @@ void flash_fwd_kernel(const FlashArgs a) {
   const float* brow = (MASKED && a.key_bias) ? a.key_bias + (int64_t)b * a.key_mask_stride : nullptr;
 
   if (n_tiles > 0) {
-    u32x4 kst[kLoadsPerWave], vst[kLoadsPerWave];
-    // Prologue: K0 -> K buffer 0, V0 -> V buffer 0, K1 -> K buffer 1 and a
-    // zeroed V buffer 2 that stands in for "V_{-1}" (paired with P = 0).
-    gload(kg, a.ks[1], 0, kst);
-    gload(vg, a.vs[1], 0, vst);
-    lstore(kKBuf, kst);
-    lstore(kVBuf, vst);
-    gload(kg, a.ks[1], min(1, n_tiles - 1), kst);
-    lstore(kKBuf + kTileBytes, kst);
+    // Tile j of K lives in K buffer j % 3 and tile j of V in V buffer j % 3;
+    // V buffer 2 stands in for "V_{-1}" (zeros, paired with P = 0 in
+    // iteration 0). Iteration t issues K_{t+3} and V_{t+1}, two iterations
+    // before they are read, so their latency is hidden.
+    stage(kg, a.ks[1], 0, kKBuf);
+    stage(kg, a.ks[1], min(1, n_tiles - 1), kKBuf + kTileBytes);
+    stage(kg, a.ks[1], min(2, n_tiles - 1), kKBuf + 2 * kTileBytes);
+    stage(vg, a.vs[1], 0, kVBuf);
 #pragma unroll
     for (int p = 0; p < kTileBytes / (kThreads * 16); ++p)
       *(VX_LDS u32x4*)(lds + kVBuf + 2 * kTileBytes + (p * kThreads + threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
+    wait_vmem<2 * kLoadsPerWave>();  // K_0 and K_1 have landed
     __syncthreads();
     f32x16 S[2];
     qk(kKBuf, S);
@@ -199,14 +220,18 @@ void flash_fwd_kernel(const FlashArgs a) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) Pp[kb][j] = bf16x8{};
 
-    int kb_cur = 1;   // K buffer holding K_{t+1}
-    int vb_prev = 2;  // V buffer holding V_{t-1}
+    int kb_cur = 1;   // K buffer holding K_{t+1}  (= (t+1) % 3)
+    int vb_prev = 2;  // V buffer holding V_{t-1}  (= (t+2) % 3)
     for (int t = 0; t < n_tiles; ++t) {
-      // LDS holds K_{t+1} in K buffer kb_cur, V_{t-1} in V buffer vb_prev and
-      // V_t in V buffer (vb_prev + 1) % 3.
+      // Tiles issued two iterations ago (K_{t+1}, V_{t-1}) have landed once
+      // only the previous iteration's 2 * kLoadsPerWave DMA instructions may
+      // still be outstanding; the barrier then publishes them, and it also
+      // frees K buffer t % 3 (K_t, read by QK(t) last iteration) and V buffer
+      // (t+1) % 3 (V_{t-2}) for this iteration's prefetch.
+      wait_vmem<2 * kLoadsPerWave>();
       __syncthreads();
-      gload(kg, a.ks[1], min(t + 2, n_tiles - 1), kst);
-      gload(vg, a.vs[1], min(t + 1, n_tiles - 1), vst);
+      const int kb_next = kb_cur == 0 ? 2 : kb_cur - 1;  // t % 3
+      const int vb_next = vb_prev == 2 ? 1 : (vb_prev == 1 ? 0 : 2);  // (t+1) % 3
 
       // ---- key masks. Tiles that hold a masked key (the tail tile, a
       // key_valid hole, any key_bias) take the scores to log2 units here,
@@ -232,6 +257,8 @@ void flash_fwd_kernel(const FlashArgs a) {
         }
         slow = slow || brow != nullptr;
       }
+      stage(kg, a.ks[1], min(t + 3, n_tiles - 1), kKBuf + kb_next * kTileBytes);
+      stage(vg, a.vs[1], min(t + 1, n_tiles - 1), kVBuf + vb_next * kTileBytes);
       float cc = c;
       if (slow) {
         cc = 1.0f;
@@ -330,19 +357,18 @@ void flash_fwd_kernel(const FlashArgs a) {
       l_run += l_tile;
 
       // ---- publish the prefetched tiles (read by everyone after the next barrier).
-      const int vb_next = vb_prev == 0 ? 2 : vb_prev - 1;  // buffer of V_{t-2}, free now
-      lstore(kKBuf + (kb_cur ^ 1) * kTileBytes, kst);
-      lstore(kVBuf + vb_next * kTileBytes, vst);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         S[kb] = Sn[kb];
 #pragma unroll
         for (int j = 0; j < 2; ++j) Pp[kb][j] = P[kb][j];
       }
-      kb_cur ^= 1;
+      kb_cur = kb_cur == 2 ? 0 : kb_cur + 1;
       vb_prev = vb_prev == 2 ? 0 : vb_prev + 1;
     }
     // ---- PV of the last tile (V_{n-1} sits in V buffer vb_prev now).
+    wait_vmem<0>();
+    __syncthreads();
     pv(kVBuf + vb_prev * kTileBytes, Pp, O);
   }
 
