@@ -43,7 +43,11 @@ NA_CASES = [
     ((1, 3, 9, 11, 1), (2, 4, 6), 34),     # even windows
     ((1, 2, 3, 4, 2), (5, 9, 9), 35),      # every window clamped: full attention
     ((1, 3, 4, 30, 1), (1, 1, 25), 36),    # wide x window (two 16-key segments)
-    ((1, 2, 4, 70, 1), (1, 3, 57), 37),    # widest supported x window
+    ((1, 2, 4, 70, 1), (1, 3, 57), 37),    # widest supported x window (per-wave kernel)
+    ((1, 3, 10, 40, 2), (3, 11, 11), 41),  # 32-slot x windows (LTX-2.5 stage-5 shape family)
+    ((1, 4, 17, 33, 1), (3, 5, 13), 42),
+    ((2, 5, 9, 65, 2), (5, 3, 9), 43),     # ragged workgroup bricks along y and x
+    ((1, 2, 20, 8, 1), (2, 9, 3), 44),
 ]
 
 

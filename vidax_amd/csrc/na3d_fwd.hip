@@ -36,7 +36,7 @@ __device__ __forceinline__ int window_start(int i, int len, int k) {
 }
 
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
-void na3d_fwd_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
+void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[kWaves * 2 * kChunkBytes];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -240,15 +240,280 @@ void na3d_fwd_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Row-streaming kernel (kw' <= 25). A workgroup of 8 waves owns a brick of
+// 1 (t) x 8 (y) x 32 (x) queries of one head: waves 0-3 take y rows 0-3 and
+// waves 4-7 rows 4-7, each wave 8 consecutive x. The union of the brick's
+// windows is kt' x NY key rows (t', y') of NX consecutive x positions. The
+// workgroup streams those rows two at a time through LDS with the DMA path
+// (NBUF-deep ring, issued NBUF-1 steps ahead); each wave reads the SEG-wide
+// window of x positions it needs from every row: one 32-key chunk per step
+// for SEG = 16 (two rows x 16), two chunks for SEG = 32 (one row each).
+// Waves whose y window misses both rows of a step skip its math.
+
+template <int SEG, int NBUF>
+struct RowCfg {
+  static constexpr int kWaves = 8;
+  static constexpr int kThreads = kWaves * 64;
+  static constexpr int kBrickY = 8, kBrickX = 32;
+  static constexpr int kNS = SEG == 16 ? 48 : 64;             // key slots per LDS row
+  static constexpr int kRowTensorBytes = kNS * kRowBytes;     // one key row of K (or V)
+  static constexpr int kStepBytes = 4 * kRowTensorBytes;      // K row0, K row1, V row0, V row1
+  static constexpr int kSmem = NBUF * kStepBytes;
+  static constexpr int kDmaPerWave = kNS / kWaves;            // 1 KiB DMA copies per step per wave
+};
+
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_row) {
+  // Issued as inline assembly so the compiler does not wait for the copy
+  // before every later LDS read; the kernel orders it with s_waitcnt and a
+  // barrier before any wave reads the destination.
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_row))
+               : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+template <int SEG, int NBUF>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void na3d_rows_kernel(const Na3dArgs a, int n_yb, int n_xb) {
+  using C = RowCfg<SEG, NBUF>;
+  constexpr int RT = C::kRowTensorBytes;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[C::kSmem];
+  VX_LDS unsigned char* const lds = (VX_LDS unsigned char*)smem;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int hf = lane >> 5;
+  const int col = lane & 31;
+
+  int bid = blockIdx.x;
+  const int xb = bid % n_xb;
+  bid /= n_xb;
+  const int yb = bid % n_yb;
+  const int t = bid / n_yb;
+  const int head = blockIdx.y;
+  const int b = blockIdx.z;
+  const int T = a.T, Hs = a.Hs, W = a.W, kt = a.kt, kh = a.kh, kw = a.kw;
+  const int y0 = yb * C::kBrickY, x0 = xb * C::kBrickX;
+
+  // ---- the workgroup's key rows.
+  const int t_lo = window_start(t, T, kt);
+  const int Y_lo = window_start(y0, Hs, kh);
+  const int NY = window_start(min(y0 + C::kBrickY - 1, Hs - 1), Hs, kh) + kh - Y_lo;
+  const int X_lo = window_start(x0, W, kw);
+  const int nrows = kt * NY;
+  const int n_steps = (nrows + 1) / 2;
+
+  // ---- this wave's queries: y rows yq0..yq0+3, x columns xq0..xq0+7.
+  const int yq0 = y0 + 4 * (wave >> 2);
+  const int xq0 = x0 + 8 * (wave & 3);
+  const bool wave_live = yq0 < Hs && xq0 < W;
+  const int yw_lo = window_start(min(yq0, Hs - 1), Hs, kh) - Y_lo;          // wave's y window, in
+  const int yw_hi = window_start(min(yq0 + 3, Hs - 1), Hs, kh) + kh - Y_lo;  // box rows
+  const int ox = window_start(min(xq0, W - 1), W, kw) - X_lo;  // wave's first x slot
+
+  // ---- this lane's query and its window.
+  const int yq = yq0 + col / 8, xq = xq0 + col % 8;
+  const bool q_in = yq < Hs && xq < W;
+  const int yqc = min(yq, Hs - 1), xqc = min(xq, W - 1);
+  const int sy = window_start(yqc, Hs, kh) - Y_lo;
+  const int sx = window_start(xqc, W, kw) - X_lo - ox;  // in [0, SEG - kw]
+  const uint64_t xmask = (((1ull << kw) - 1) << sx) >> (hf * 4);
+
+  const int64_t tok_stride = (int64_t)a.NH * kD;
+  const int64_t head_off = (int64_t)b * T * Hs * W * tok_stride + (int64_t)head * kD;
+  const bf16* qg = (const bf16*)a.q + head_off;
+  const bf16* kg = (const bf16*)a.k + head_off;
+  const bf16* vg = (const bf16*)a.v + head_off;
+  bf16* og = (bf16*)a.o + head_off;
+  auto token = [&](int tt, int yy, int xx) -> int64_t { return ((int64_t)tt * Hs + yy) * W + xx; };
+
+  bf16x8 qr[8];
+  {
+    const bf16* p = qg + token(t, yqc, xqc) * tok_stride + hf * 8;
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
+  }
+
+  // ---- DMA of step s into ring slot s % NBUF: copy i of the step covers
+  // tensor i / (kNS/2), row i / (kNS/4) % 2 and x slots 4*(i % (kNS/4)) + 0..3.
+  const int srow = lane >> 4, scol = lane & 15;
+  auto issue_step = [&](int s) {
+    const int slot = s % NBUF;
+#pragma unroll
+    for (int p = 0; p < C::kDmaPerWave; ++p) {
+      const int i = wave * C::kDmaPerWave + p;
+      const int tensor = i / (C::kNS / 2);
+      const int rowsel = (i / (C::kNS / 4)) & 1;
+      const int pos = 4 * (i % (C::kNS / 4)) + srow;
+      const int r = min(2 * s + rowsel, nrows - 1);
+      const int tr = r / NY, yr = r - tr * NY;
+      const int64_t tok = token(t_lo + tr, Y_lo + yr, min(X_lo + pos, W - 1));
+      const bf16* src = (tensor ? vg : kg) + tok * tok_stride + ((scol ^ row_swizzle(pos)) * 8);
+      const int dst = slot * C::kStepBytes + (2 * tensor + rowsel) * RT + (pos - srow) * kRowBytes;
+      lds_dma16(src, lds_base + dst);
+    }
+  };
+
+  // ---- per-lane LDS offsets. K fragment: key col of the chunk.
+  int kbase, ksw;
+  if (SEG == 16) {
+    const int pos = ox + (col & 15);
+    kbase = (col >> 4) * RT + pos * kRowBytes;
+    ksw = row_swizzle(pos);
+  } else {
+    const int pos = ox + col;
+    kbase = pos * kRowBytes;
+    ksw = row_swizzle(pos);
+  }
+  int koff[4];
+#pragma unroll
+  for (int d4 = 0; d4 < 4; ++d4) koff[d4] = kbase + (((2 * d4 + hf) ^ ksw) * 16);
+  // V transpose reads: key 16j + 8e + 4hf + vr of the chunk.
+  const int i16 = lane & 15;
+  const int vr = i16 >> 2, vc = i16 & 3, dh = (lane >> 4) & 1;
+  int voff[2][2];  // [e][db & 1]
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int pos = ox + 8 * e + 4 * hf + vr;
+    const int sw = row_swizzle(pos);
+#pragma unroll
+    for (int db1 = 0; db1 < 2; ++db1)
+      voff[e][db1] = 2 * RT + pos * kRowBytes + (((4 * db1 + 2 * dh + (vc >> 1)) ^ sw) * 16) + (vc & 1) * 8;
+  }
+
+  f32x16 O[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) O[db] = f32x16{};
+  float m_run = kNegBig, l_run = 0.f;
+  const float c2 = a.scale * kLog2e;
+
+  // One 32-key chunk: K rows at kaddr + koff, V rows at vaddr + voff; rows
+  // r0 (keys 0-15) and r1 (keys 16-31) of the box, x slots from this
+  // wave's window (SEG = 16), or one row r0 for all 32 keys (SEG = 32).
+  auto chunk = [&](const VX_LDS unsigned char* kaddr, const VX_LDS unsigned char* vaddr, int r0, int r1) {
+    f32x16 S = f32x16{};
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) {
+      const bf16x8 kf = *(const VX_LDS bf16x8*)(kaddr + koff[ds & 3] + (ds >> 2) * 128);
+      S = mfma32x32x16(kf, qr[ds], S);
+    }
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const int r = h2 == 0 ? r0 : r1;
+      const int yr = r % NY;
+      const bool row_ok = r < nrows && (unsigned)(yr - sy) < (unsigned)kh;
+      const uint64_t xm = row_ok ? (xmask >> (SEG == 16 ? 0 : 16 * h2)) : 0ull;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int bit = (i >> 2) * 8 + (i & 3);
+        const bool ok = (xm >> bit) & 1ull;
+        S[8 * h2 + i] = ok ? S[8 * h2 + i] * c2 : -__builtin_inff();
+      }
+    }
+    float mx = S[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = __builtin_fmaxf(mx, S[i]);
+    const float ms = halves_max(mx);
+    if (__builtin_amdgcn_ballot_w64(ms > m_run + kRescaleSlack) != 0) {
+      const float mn = __builtin_fmaxf(m_run, ms);
+      const float alpha = fast_exp2(m_run - mn);
+      m_run = mn;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) O[db] *= alpha;
+    }
+    bf16x8 P[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      bf16x8 pv;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) pv[r] = (bf16)fast_exp2(S[8 * j + r] - m_run);
+      P[j] = pv;
+      l_run = sum8(pv, l_run);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int jo = SEG == 16 ? j * RT : j * 16 * kRowBytes;
+        const VX_LDS unsigned char* p0 = vaddr + jo + voff[0][db & 1] + (db >> 1) * 128;
+        const VX_LDS unsigned char* p1 = vaddr + jo + voff[1][db & 1] + (db >> 1) * 128;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p0);
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p1);
+        const bf16x8 vf = concat(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi));
+        O[db] = mfma32x32x16(vf, P[j], O[db]);
+      }
+  };
+
+  // ---- prologue: the first NBUF-1 steps in flight.
+#pragma unroll
+  for (int s = 0; s < NBUF - 1; ++s) issue_step(min(s, n_steps - 1));
+  for (int s = 0; s < n_steps; ++s) {
+    // Step s landed once only the NBUF-2 most recent steps may be in flight.
+    wait_vmem<C::kDmaPerWave * (NBUF - 2)>();
+    __syncthreads();
+    // The slot of step s-1 is free now: refill it with step s+NBUF-1.
+    issue_step(min(s + NBUF - 1, n_steps - 1));
+    const int r0 = 2 * s, r1 = 2 * s + 1;
+    const int y0r = r0 % NY, y1r = r1 % NY;
+    const bool live = wave_live && ((y0r >= yw_lo && y0r < yw_hi) || (r1 < nrows && y1r >= yw_lo && y1r < yw_hi));
+    if (live) {
+      const VX_LDS unsigned char* base = lds + (s % NBUF) * C::kStepBytes;
+      if (SEG == 16) {
+        chunk(base, base, r0, r1);
+      } else {
+        chunk(base, base, r0, r0);
+        chunk(base + RT, base + RT, r1, r1);
+      }
+    }
+  }
+  wait_vmem<0>();
+
+  const float lt = halves_sum(l_run);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (q_in) {
+    bf16* orow = og + token(t, yq, xq) * tok_stride;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        bf16x4 ov;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[e] = (bf16)(O[db][g * 4 + e] * inv);
+        *(bf16x4*)(orow + db * 32 + g * 8 + hf * 4) = ov;
+      }
+  }
+}
+
 }  // namespace
 
 int launch_na3d_fwd(const Na3dArgs& a, void* stream) {
   if (a.D != kD) return (int)hipErrorNotSupported;
+  hipStream_t st = (hipStream_t)stream;
+  if (a.kw <= 25) {
+    const int n_yb = (a.Hs + 7) / 8;
+    const int n_xb = (a.W + 31) / 32;
+    dim3 grid((unsigned)a.T * n_yb * n_xb, a.NH, a.B);
+    if (a.kw <= 9)
+      hipLaunchKernelGGL((na3d_rows_kernel<16, 3>), grid, dim3(512), 0, st, a, n_yb, n_xb);
+    else
+      hipLaunchKernelGGL((na3d_rows_kernel<32, 2>), grid, dim3(512), 0, st, a, n_yb, n_xb);
+    return (int)hipGetLastError();
+  }
   const int n_yb = (a.Hs + kBrickY - 1) / kBrickY;
   const int n_xb = (a.W + kBrickX - 1) / kBrickX;
   const int n_xg = (n_xb + kWaves - 1) / kWaves;
   dim3 grid((unsigned)a.T * n_yb * n_xg, a.NH, a.B);
-  hipLaunchKernelGGL(na3d_fwd_kernel, grid, dim3(kWaves * 64), 0, (hipStream_t)stream, a, n_yb, n_xb, n_xg);
+  hipLaunchKernelGGL(na3d_wave_kernel, grid, dim3(kWaves * 64), 0, st, a, n_yb, n_xb, n_xg);
   return (int)hipGetLastError();
 }
 
