@@ -200,8 +200,9 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       bf16x8 pv;
+      const float mneg = -m_run;
 #pragma unroll
-      for (int r = 0; r < 8; ++r) pv[r] = (bf16)fast_exp2(S[8 * j + r] - m_run);
+      for (int r = 0; r < 8; ++r) pv[r] = (bf16)fast_exp2(S[8 * j + r] + mneg);
       P[j] = pv;
       l_run = sum8(pv, l_run);
     }
@@ -257,11 +258,12 @@ struct RowCfg {
   static constexpr int kWaves = 8;
   static constexpr int kThreads = kWaves * 64;
   static constexpr int kBrickY = 8, kBrickX = 32;
-  static constexpr int kNS = SEG == 16 ? 48 : 64;             // key slots per LDS row
+  static constexpr int kNS = SEG == 16 ? 40 : 64;             // key slots per LDS row
   static constexpr int kRowTensorBytes = kNS * kRowBytes;     // one key row of K (or V)
   static constexpr int kStepBytes = 4 * kRowTensorBytes;      // K row0, K row1, V row0, V row1
   static constexpr int kSmem = NBUF * kStepBytes;
-  static constexpr int kDmaPerWave = kNS / kWaves;            // 1 KiB DMA copies per step per wave
+  static constexpr int kDmaTotal = kNS;                        // 1 KiB DMA copies per step
+  static constexpr int kDmaPerWave = (kDmaTotal + kWaves - 1) / kWaves;  // per wave (last ones repeat)
 };
 
 __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_row) {
@@ -290,16 +292,29 @@ void na3d_rows_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int hf = lane >> 5;
   const int col = lane & 31;
 
-  int bid = blockIdx.x;
-  const int xb = bid % n_xb;
-  bid /= n_xb;
-  const int yb = bid % n_yb;
-  const int t = bid / n_yb;
-  const int head = blockIdx.y;
+  // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
+  // L2). With heads % 8 == 0 the linear workgroup id is remapped so that XCD
+  // x walks the bricks of heads x, x+8, ... in order: the workgroups resident
+  // on one XCD then cover neighbouring bricks of one head and share their
+  // key rows in that XCD's L2.
+  const int n_bricks = a.T * n_yb * n_xb;
+  int brick, head;
+  if ((a.NH & 7) == 0) {
+    const int lin = blockIdx.y * n_bricks + blockIdx.x;  // launch order within a batch item
+    const int xcd = lin & 7, j = lin >> 3;
+    head = xcd + 8 * (j / n_bricks);
+    brick = j % n_bricks;
+  } else {
+    head = blockIdx.y;
+    brick = blockIdx.x;
+  }
+  const int xb = brick % n_xb;
+  const int yb = (brick / n_xb) % n_yb;
+  const int t = brick / (n_xb * n_yb);
   const int b = blockIdx.z;
   const int T = a.T, Hs = a.Hs, W = a.W, kt = a.kt, kh = a.kh, kw = a.kw;
   const int y0 = yb * C::kBrickY, x0 = xb * C::kBrickX;
@@ -326,7 +341,14 @@ void na3d_rows_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   const int yqc = min(yq, Hs - 1), xqc = min(xq, W - 1);
   const int sy = window_start(yqc, Hs, kh) - Y_lo;
   const int sx = window_start(xqc, W, kw) - X_lo - ox;  // in [0, SEG - kw]
-  const uint64_t xmask = (((1ull << kw) - 1) << sx) >> (hf * 4);
+  // Per score register i: +inf if its key's x slot lies in this lane's
+  // window, -inf otherwise (the mask is a v_min3 with the row limit below).
+  float xlim[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int p = (SEG == 16 ? ((i >> 2) & 1) * 8 : (i >> 2) * 8) + hf * 4 + (i & 3);
+    xlim[i] = (unsigned)(p - sx) < (unsigned)kw ? __builtin_inff() : -__builtin_inff();
+  }
 
   const int64_t tok_stride = (int64_t)a.NH * kD;
   const int64_t head_off = (int64_t)b * T * Hs * W * tok_stride + (int64_t)head * kD;
@@ -345,20 +367,38 @@ void na3d_rows_kernel(const Na3dArgs a, int n_yb, int n_xb) {
 
   // ---- DMA of step s into ring slot s % NBUF: copy i of the step covers
   // tensor i / (kNS/2), row i / (kNS/4) % 2 and x slots 4*(i % (kNS/4)) + 0..3.
+  // The lane-dependent part of every copy's source address (x position and
+  // swizzled 16-byte chunk) is fixed for the workgroup; only the row token
+  // changes per step and is computed once per step in scalar registers.
   const int srow = lane >> 4, scol = lane & 15;
+  int64_t dma_off[C::kDmaPerWave];
+#pragma unroll
+  for (int p = 0; p < C::kDmaPerWave; ++p) {
+    // copies past kDmaTotal repeat the last one (same bytes, same place), so
+    // every wave issues the same number of copies per step
+    const int i = min(wave * C::kDmaPerWave + p, C::kDmaTotal - 1);
+    const int pos = 4 * (i % (C::kNS / 4)) + srow;
+    dma_off[p] = (int64_t)min(X_lo + pos, W - 1) * tok_stride + ((scol ^ row_swizzle(pos)) * 8);
+  }
+  // (t', y') of box row r as a token offset, and its y index within the box.
+  auto row_token = [&](int r, int& yr) -> int64_t {
+    const int tr = r / NY;
+    yr = r - tr * NY;
+    return (((int64_t)(t_lo + tr) * Hs + (Y_lo + yr)) * W) * tok_stride;
+  };
   auto issue_step = [&](int s) {
     const int slot = s % NBUF;
+    int yr_unused;
+    const int64_t rt0 = row_token(min(2 * s, nrows - 1), yr_unused);
+    const int64_t rt1 = row_token(min(2 * s + 1, nrows - 1), yr_unused);
 #pragma unroll
     for (int p = 0; p < C::kDmaPerWave; ++p) {
-      const int i = wave * C::kDmaPerWave + p;
+      const int i = min(wave * C::kDmaPerWave + p, C::kDmaTotal - 1);
       const int tensor = i / (C::kNS / 2);
       const int rowsel = (i / (C::kNS / 4)) & 1;
-      const int pos = 4 * (i % (C::kNS / 4)) + srow;
-      const int r = min(2 * s + rowsel, nrows - 1);
-      const int tr = r / NY, yr = r - tr * NY;
-      const int64_t tok = token(t_lo + tr, Y_lo + yr, min(X_lo + pos, W - 1));
-      const bf16* src = (tensor ? vg : kg) + tok * tok_stride + ((scol ^ row_swizzle(pos)) * 8);
-      const int dst = slot * C::kStepBytes + (2 * tensor + rowsel) * RT + (pos - srow) * kRowBytes;
+      const int g = i % (C::kNS / 4);
+      const bf16* src = (tensor ? vg : kg) + (rowsel ? rt1 : rt0) + dma_off[p];
+      const int dst = slot * C::kStepBytes + (2 * tensor + rowsel) * RT + 4 * g * kRowBytes;
       lds_dma16(src, lds_base + dst);
     }
   };
@@ -399,30 +439,30 @@ void na3d_rows_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   // One 32-key chunk: K rows at kaddr + koff, V rows at vaddr + voff; rows
   // r0 (keys 0-15) and r1 (keys 16-31) of the box, x slots from this
   // wave's window (SEG = 16), or one row r0 for all 32 keys (SEG = 32).
-  auto chunk = [&](const VX_LDS unsigned char* kaddr, const VX_LDS unsigned char* vaddr, int r0, int r1) {
+  // ok0/ok1: the chunk's first / second 16 keys come from an existing box
+  // row; yr0/yr1: those rows' y index within the box.
+  auto chunk = [&](const VX_LDS unsigned char* kaddr, const VX_LDS unsigned char* vaddr, bool ok0, int yr0,
+                   bool ok1, int yr1) {
     f32x16 S = f32x16{};
 #pragma unroll
     for (int ds = 0; ds < 8; ++ds) {
       const bf16x8 kf = *(const VX_LDS bf16x8*)(kaddr + koff[ds & 3] + (ds >> 2) * 128);
       S = mfma32x32x16(kf, qr[ds], S);
     }
+    // window mask: keys outside this lane's y or x window -> -inf
+    float rlim[2];
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
-      const int r = h2 == 0 ? r0 : r1;
-      const int yr = r % NY;
-      const bool row_ok = r < nrows && (unsigned)(yr - sy) < (unsigned)kh;
-      const uint64_t xm = row_ok ? (xmask >> (SEG == 16 ? 0 : 16 * h2)) : 0ull;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int bit = (i >> 2) * 8 + (i & 3);
-        const bool ok = (xm >> bit) & 1ull;
-        S[8 * h2 + i] = ok ? S[8 * h2 + i] * c2 : -__builtin_inff();
-      }
+      const int yr = h2 == 0 ? yr0 : yr1;
+      const bool row_ok = (h2 == 0 ? ok0 : ok1) && (unsigned)(yr - sy) < (unsigned)kh;
+      rlim[h2] = row_ok ? __builtin_inff() : -__builtin_inff();
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) S[i] = __builtin_fminf(__builtin_fminf(S[i], xlim[i]), rlim[i >> 3]);
     float mx = S[0];
 #pragma unroll
     for (int i = 1; i < 16; ++i) mx = __builtin_fmaxf(mx, S[i]);
-    const float ms = halves_max(mx);
+    const float ms = halves_max(mx) * c2;  // scores stay raw; c2 folds into the exp argument
     if (__builtin_amdgcn_ballot_w64(ms > m_run + kRescaleSlack) != 0) {
       const float mn = __builtin_fmaxf(m_run, ms);
       const float alpha = fast_exp2(m_run - mn);
@@ -435,8 +475,9 @@ void na3d_rows_kernel(const Na3dArgs a, int n_yb, int n_xb) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       bf16x8 pv;
+      const float mneg = -m_run;
 #pragma unroll
-      for (int r = 0; r < 8; ++r) pv[r] = (bf16)fast_exp2(S[8 * j + r] - m_run);
+      for (int r = 0; r < 8; ++r) pv[r] = (bf16)fast_exp2(__builtin_fmaf(S[8 * j + r], c2, mneg));
       P[j] = pv;
       l_run = sum8(pv, l_run);
     }
@@ -463,16 +504,18 @@ void na3d_rows_kernel(const Na3dArgs a, int n_yb, int n_xb) {
     __syncthreads();
     // The slot of step s-1 is free now: refill it with step s+NBUF-1.
     issue_step(min(s + NBUF - 1, n_steps - 1));
-    const int r0 = 2 * s, r1 = 2 * s + 1;
-    const int y0r = r0 % NY, y1r = r1 % NY;
-    const bool live = wave_live && ((y0r >= yw_lo && y0r < yw_hi) || (r1 < nrows && y1r >= yw_lo && y1r < yw_hi));
+    int y0r, y1r;
+    (void)row_token(2 * s, y0r);
+    (void)row_token(min(2 * s + 1, nrows - 1), y1r);
+    const bool ok1 = 2 * s + 1 < nrows;
+    const bool live = wave_live && ((y0r >= yw_lo && y0r < yw_hi) || (ok1 && y1r >= yw_lo && y1r < yw_hi));
     if (live) {
       const VX_LDS unsigned char* base = lds + (s % NBUF) * C::kStepBytes;
       if (SEG == 16) {
-        chunk(base, base, r0, r1);
+        chunk(base, base, true, y0r, ok1, y1r);
       } else {
-        chunk(base, base, r0, r0);
-        chunk(base + RT, base + RT, r1, r1);
+        chunk(base, base, true, y0r, true, y0r);
+        chunk(base + RT, base + RT, ok1, y1r, ok1, y1r);
       }
     }
   }
@@ -504,7 +547,7 @@ int launch_na3d_fwd(const Na3dArgs& a, void* stream) {
     const int n_xb = (a.W + 31) / 32;
     dim3 grid((unsigned)a.T * n_yb * n_xb, a.NH, a.B);
     if (a.kw <= 9)
-      hipLaunchKernelGGL((na3d_rows_kernel<16, 3>), grid, dim3(512), 0, st, a, n_yb, n_xb);
+      hipLaunchKernelGGL((na3d_rows_kernel<16, 4>), grid, dim3(512), 0, st, a, n_yb, n_xb);
     else
       hipLaunchKernelGGL((na3d_rows_kernel<32, 2>), grid, dim3(512), 0, st, a, n_yb, n_xb);
     return (int)hipGetLastError();
