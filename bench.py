@@ -114,7 +114,7 @@ def _cpu_baseline(kind, p, budget_s=12.0):
             O.attention(q, k, v, acc=np.float32, q_block=256)
             reps += 1
             el = time.perf_counter() - t0
-            if el >= budget_s or reps >= 64:
+            if el >= budget_s or reps >= 1000:
                 break
         flops = 4.0 * 128 * rows * Sk * H * reps
         sample = (f"oracle fp32 (numpy/BLAS) attention, {reps} x (1 head x {rows} query rows x "
@@ -132,7 +132,7 @@ def _cpu_baseline(kind, p, budget_s=12.0):
         O.na3d(q, k, v, p["kernel"], acc=np.float32)
         reps += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 16:
+        if el >= budget_s or reps >= 200:
             break
     kt, kh, kw = (min(p["kernel"][0], T), min(p["kernel"][1], p["Hs"]), min(p["kernel"][2], p["W"]))
     flops = 4.0 * 2 * T * p["Hs"] * p["W"] * kt * kh * kw * 128 * reps
@@ -142,12 +142,31 @@ def _cpu_baseline(kind, p, budget_s=12.0):
 
 
 def _traffic(kernel_name, workload):
+    """HBM bytes per launch of the kernel on this workload, measured with the
+    FETCH_SIZE and WRITE_SIZE counters (two separate profiler passes) and
+    scaled by the same counters' reading for a plain copy of known size."""
     try:
         with open(TRAFFIC_FILE) as f:
-            rec = json.load(f)
-        return rec.get(workload, {}).get(kernel_name, {}).get("hbm_bytes_per_launch")
+            rec = json.load(f).get("workloads", {}).get(workload, {})
     except (OSError, ValueError):
         return None
+    if rec.get("kernel") != kernel_name:
+        return None
+    return rec.get("hbm_bytes_per_launch")
+
+
+def _copy_calibration(mib, steps):
+    """A plain device copy of known size, timed the same way; profiled with the
+    same counters it gives the bytes-per-KiB factor of FETCH_SIZE/WRITE_SIZE."""
+    import torch
+    n = int(mib) << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": steps}), flush=True)
+    return 0
 
 
 def main(argv=None):
@@ -158,6 +177,8 @@ def main(argv=None):
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB --steps times")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -165,6 +186,9 @@ def main(argv=None):
               "--gpus N with N > 1 is not supported (how the path would shard is "
               "described in DESIGN.md)", file=sys.stderr)
         return 2
+
+    if args.copy_calibration_mib:
+        return _copy_calibration(args.copy_calibration_mib, args.steps)
 
     import torch
     import vidax_amd
@@ -180,7 +204,7 @@ def main(argv=None):
 
         def step():
             vidax_amd.flash_attention(q, k, v, out=out, **kw)
-        kernel_name = "flash_fwd_kernel"
+        kernel_name = "flash_fwd_kernel<true>" if kw else "flash_fwd_kernel<false>"
     else:
         g = torch.Generator(device=dev)
         g.manual_seed(p["seed"])
@@ -194,7 +218,7 @@ def main(argv=None):
 
         def step():
             na3d_attention(q, k, v, p["kernel"], out=out)
-        kernel_name = "na3d_fwd_kernel"
+        kernel_name = vidax_amd.natten.na3d_kernel_name(p["W"], p["kernel"][2])
 
     for _ in range(args.warmup):
         step()
