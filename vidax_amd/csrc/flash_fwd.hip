@@ -97,6 +97,7 @@ void flash_fwd_kernel(const FlashArgs a) {
 
   int kv_end = a.Sk;
   if (a.kv_len != nullptr) kv_end = min(max(a.kv_len[b], 0), a.Sk);
+  kv_end = __builtin_amdgcn_readfirstlane(kv_end);  // uniform: scalar loop control
   const int n_tiles = (kv_end + kBN - 1) / kBN;
   const float c = a.scale * kLog2e;
 
@@ -132,15 +133,33 @@ void flash_fwd_kernel(const FlashArgs a) {
   // (global_load_lds_dwordx4): each wave instruction fills 4 consecutive
   // 256-byte rows, lane L landing at byte 16*L, so lane L fetches the global
   // chunk that the swizzle places there. kLoadsPerWave instructions per tile.
+  // Tiles that lie wholly below kv_end add a uniform tile offset to per-lane
+  // row pointers computed once; the tail tile clamps its rows to kv_end - 1.
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
-  auto stage = [&](const bf16* base, int64_t sstride, int t, int buf_off) {
+  const bf16* klane[kLoadsPerWave];
+  const bf16* vlane[kLoadsPerWave];
 #pragma unroll
-    for (int p = 0; p < kLoadsPerWave; ++p) {
-      const int r0 = (wave * kLoadsPerWave + p) * 4;
-      const int r = r0 + srow;
-      const int key = min(t * kBN + r, kv_end - 1);
-      const bf16* src = base + (int64_t)key * sstride + ((scol ^ row_swizzle(r)) * 8);
-      lds_dma16(src, lds_base + buf_off + r0 * kRowBytes);
+  for (int p = 0; p < kLoadsPerWave; ++p) {
+    const int r = (wave * kLoadsPerWave + p) * 4 + srow;
+    klane[p] = kg + (int64_t)r * a.ks[1] + ((scol ^ row_swizzle(r)) * 8);
+    vlane[p] = vg + (int64_t)r * a.vs[1] + ((scol ^ row_swizzle(r)) * 8);
+  }
+  auto stage = [&](const bf16* base, const bf16* const (&lanep)[kLoadsPerWave], int64_t sstride, int t,
+                   int buf_off) {
+    if ((t + 1) * kBN <= kv_end) {
+      const int64_t off = (int64_t)(t * kBN) * sstride;
+#pragma unroll
+      for (int p = 0; p < kLoadsPerWave; ++p)
+        lds_dma16(lanep[p] + off, lds_base + buf_off + (wave * kLoadsPerWave + p) * 4 * kRowBytes);
+    } else {
+#pragma unroll
+      for (int p = 0; p < kLoadsPerWave; ++p) {
+        const int r0 = (wave * kLoadsPerWave + p) * 4;
+        const int r = r0 + srow;
+        const int key = min(t * kBN + r, kv_end - 1);
+        const bf16* src = base + (int64_t)key * sstride + ((scol ^ row_swizzle(r)) * 8);
+        lds_dma16(src, lds_base + buf_off + r0 * kRowBytes);
+      }
     }
   };
 
@@ -203,10 +222,10 @@ void flash_fwd_kernel(const FlashArgs a) {
     // V buffer 2 stands in for "V_{-1}" (zeros, paired with P = 0 in
     // iteration 0). Iteration t issues K_{t+3} and V_{t+1}, two iterations
     // before they are read, so their latency is hidden.
-    stage(kg, a.ks[1], 0, kKBuf);
-    stage(kg, a.ks[1], min(1, n_tiles - 1), kKBuf + kTileBytes);
-    stage(kg, a.ks[1], min(2, n_tiles - 1), kKBuf + 2 * kTileBytes);
-    stage(vg, a.vs[1], 0, kVBuf);
+    stage(kg, klane, a.ks[1], 0, kKBuf);
+    stage(kg, klane, a.ks[1], min(1, n_tiles - 1), kKBuf + kTileBytes);
+    stage(kg, klane, a.ks[1], min(2, n_tiles - 1), kKBuf + 2 * kTileBytes);
+    stage(vg, vlane, a.vs[1], 0, kVBuf);
 #pragma unroll
     for (int p = 0; p < kTileBytes / (kThreads * 16); ++p)
       *(VX_LDS u32x4*)(lds + kVBuf + 2 * kTileBytes + (p * kThreads + threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
@@ -222,7 +241,12 @@ void flash_fwd_kernel(const FlashArgs a) {
 
     int kb_cur = 1;   // K buffer holding K_{t+1}  (= (t+1) % 3)
     int vb_prev = 2;  // V buffer holding V_{t-1}  (= (t+2) % 3)
-    for (int t = 0; t < n_tiles; ++t) {
+    // One key tile: consumes S (scores of tile t) and Pp (probabilities of
+    // tile t-1), produces Sn (scores of tile t+1) and P (probabilities of
+    // tile t). The loop below calls it twice per trip with the two register
+    // sets swapped, so no copies are needed between tiles.
+    auto step = [&](const int t, f32x16 (&S)[2], f32x16 (&Sn)[2], const bf16x8 (&Pp)[2][2],
+                    bf16x8 (&P)[2][2]) {
       // Tiles issued two iterations ago (K_{t+1}, V_{t-1}) have landed once
       // only the previous iteration's 2 * kLoadsPerWave DMA instructions may
       // still be outstanding; the barrier then publishes them, and it also
@@ -257,8 +281,8 @@ void flash_fwd_kernel(const FlashArgs a) {
         }
         slow = slow || brow != nullptr;
       }
-      stage(kg, a.ks[1], min(t + 3, n_tiles - 1), kKBuf + kb_next * kTileBytes);
-      stage(vg, a.vs[1], min(t + 1, n_tiles - 1), kVBuf + vb_next * kTileBytes);
+      stage(kg, klane, a.ks[1], min(t + 3, n_tiles - 1), kKBuf + kb_next * kTileBytes);
+      stage(vg, vlane, a.vs[1], min(t + 1, n_tiles - 1), kVBuf + vb_next * kTileBytes);
       float cc = c;
       if (slow) {
         cc = 1.0f;
@@ -285,8 +309,8 @@ void flash_fwd_kernel(const FlashArgs a) {
       // the fragment two slots ahead, and one score's worth of softmax work for
       // tile t (speculative against the current max). sched_barrier keeps the
       // slots in this order so MFMA and VALU work of a wave overlap.
-      f32x16 Sn[2] = {f32x16{}, f32x16{}};
-      bf16x8 P[2][2];
+      Sn[0] = f32x16{};
+      Sn[1] = f32x16{};
       float l_tile = 0.f;
       float mxc = -__builtin_inff();
       float ms = 0.f;
@@ -355,16 +379,23 @@ void flash_fwd_kernel(const FlashArgs a) {
         l_tile = probs(S, cc, m_run, P);
       }
       l_run += l_tile;
-
-      // ---- publish the prefetched tiles (read by everyone after the next barrier).
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        S[kb] = Sn[kb];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) Pp[kb][j] = P[kb][j];
-      }
       kb_cur = kb_cur == 2 ? 0 : kb_cur + 1;
       vb_prev = vb_prev == 2 ? 0 : vb_prev + 1;
+    };
+
+    f32x16 S2[2];
+    bf16x8 P2[2][2];
+    int t = 0;
+    for (; t + 1 < n_tiles; t += 2) {
+      step(t, S, S2, Pp, P2);
+      step(t + 1, S2, S, P2, Pp);
+    }
+    if (t < n_tiles) {
+      step(t, S, S2, Pp, P2);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) Pp[kb][j] = P2[kb][j];
     }
     // ---- PV of the last tile (V_{n-1} sits in V buffer vb_prev now).
     wait_vmem<0>();
