@@ -19,12 +19,14 @@
 // the VALU of a wave run concurrently.
 //
 // Softmax: scores are kept in log2 units (scale * log2(e) folded into the FMA
-// that feeds v_exp_f32). The running row max is only raised when a tile's max
-// exceeds it by more than kRescaleSlack (log2 units): the probabilities are
-// computed speculatively against the current max and recomputed in the rare
-// case that a rescale is needed, which bounds the unnormalised probabilities
-// by 2^kRescaleSlack. The final division by the row sum makes the result
-// independent of the reference point.
+// that feeds v_exp_f32). The probabilities of a tile are computed
+// speculatively against the running reference point m_run, with no max pass
+// over the scores: if any probability exceeded 2^kRescaleSlack the lane's
+// partial sum of the tile exceeds kSumLimit = 2^kRescaleSlack (or is inf /
+// NaN), and only then is the tile max taken, m_run raised to it, O and l
+// rescaled and the tile's probabilities recomputed. Every probability that is
+// accumulated is therefore at most 2^kRescaleSlack. The final division by the
+// row sum makes the result independent of the reference point.
 #include "vx_gfx950.hpp"
 #include "vx_kernels.h"
 
@@ -43,6 +45,7 @@ constexpr int kKBuf = 3 * kTileBytes;         // three K tiles
 constexpr int kSmemBytes = 6 * kTileBytes;    // 96 KiB
 constexpr int kLoadsPerWave = (kBN / 4) / kWaves;  // 1 KiB wave loads per tile
 constexpr float kRescaleSlack = 8.0f;         // log2 units
+constexpr float kSumLimit = 256.0f;           // 2^kRescaleSlack
 constexpr float kNegBig = -1.0e30f;           // finite "no key seen yet" max
 
 // XOR swizzle of the 16-byte chunk index within a 256-byte LDS row. Eight
@@ -312,8 +315,6 @@ void flash_fwd_kernel(const FlashArgs a) {
       Sn[0] = f32x16{};
       Sn[1] = f32x16{};
       float l_tile = 0.f;
-      float mxc = -__builtin_inff();
-      float ms = 0.f;
       {
         const lds_u8* kb0 = lds + kKBuf + kb_cur * kTileBytes;
         const lds_u8* vb0 = lds + kVBuf + vb_prev * kTileBytes;
@@ -350,8 +351,6 @@ void flash_fwd_kernel(const FlashArgs a) {
             pk[s >> 1] = bf16x2{(bf16)pf[s - 1], (bf16)pf[s]};
             l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[s >> 1], one2, l_tile, false);
           }
-          if (s < 16) mxc = __builtin_fmaxf(__builtin_fmaxf(mxc, S[0][s]), S[1][s]);
-          if (s == 16) ms = halves_max(mxc) * cc;
           __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
@@ -365,12 +364,15 @@ void flash_fwd_kernel(const FlashArgs a) {
           }
       }
 
-      // ---- rare: the tile max exceeds the reference point by more than the
-      // slack -> move it, rescale O and l, recompute this tile's probabilities.
-      // (A NaN tile sum also takes this path; testing l_tile here keeps the
-      // speculative exp work inside the block above.)
-      if (__builtin_amdgcn_ballot_w64(ms > m_run + kRescaleSlack || is_nan_bits(l_tile)) != 0) {
-        const float mn = fmaxf(m_run, ms);
+      // ---- rare: a probability may exceed 2^kRescaleSlack (the lane's tile
+      // sum is above kSumLimit, inf or NaN; the first tile always lands here
+      // because m_run starts at kNegBig) -> raise the reference point to the
+      // tile max, rescale O and l, recompute this tile's probabilities.
+      if (__builtin_amdgcn_ballot_w64(l_tile > kSumLimit || is_nan_bits(l_tile)) != 0) {
+        float mxc = -__builtin_inff();
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mxc = __builtin_fmaxf(__builtin_fmaxf(mxc, S[0][e]), S[1][e]);
+        const float mn = fmaxf(m_run, halves_max(mxc) * cc);
         const float alpha = fast_exp2(m_run - mn);
         m_run = mn;
         l_run *= alpha;
