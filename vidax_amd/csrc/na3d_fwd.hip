@@ -27,6 +27,7 @@ constexpr int kBrickY = 4;
 constexpr int kBrickX = 8;
 constexpr int kWaves = 4;
 constexpr float kRescaleSlack = 8.0f;
+constexpr float kSumLimit = 256.0f;  // 2^kRescaleSlack
 constexpr float kNegBig = -1.0e30f;
 
 __device__ __forceinline__ int row_swizzle(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
@@ -243,27 +244,33 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
 
 
 // ---------------------------------------------------------------------------
-// Row-streaming kernel (kw' <= 25). A workgroup of 8 waves owns a brick of
-// 1 (t) x 8 (y) x 32 (x) queries of one head: waves 0-3 take y rows 0-3 and
-// waves 4-7 rows 4-7, each wave 8 consecutive x. The union of the brick's
-// windows is kt' x NY key rows (t', y') of NX consecutive x positions. The
-// workgroup streams those rows two at a time through LDS with the DMA path
-// (NBUF-deep ring, issued NBUF-1 steps ahead); each wave reads the SEG-wide
-// window of x positions it needs from every row: one 32-key chunk per step
-// for SEG = 16 (two rows x 16), two chunks for SEG = 32 (one row each).
-// Waves whose y window misses both rows of a step skip its math.
+// Pipelined row-streaming kernel (kw' <= 25). A workgroup of 4 waves owns a
+// brick of 1 (t) x 4 (y) x 32 (x) queries of one head; wave w takes the 4 y
+// rows and x columns 8w..8w+7. The union of the brick's windows is kt' x NY
+// key rows (t', y') of at most 31 + kw' consecutive x positions, and every
+// wave needs every row, so all waves run the same step sequence. The rows are
+// streamed through LDS kRows at a time (2 rows for SEG = 16, 1 for SEG = 32),
+// K and V in separate two-slot rings filled by the DMA path one step ahead;
+// each wave reads the SEG-wide x window it needs from the step's rows, one
+// 32-key chunk. Step s issues QK^T(s+1) and PV(s-1) as one 16-slot block
+// interleaved with the masking and softmax of chunk s (as in the flash
+// kernel), so the matrix cores and the VALU work of a wave overlap. With 80
+// (64) KiB of LDS and at most 256 VGPRs two workgroups share a CU.
 
-template <int SEG, int NBUF>
-struct RowCfg {
-  static constexpr int kWaves = 8;
+template <int SEG>
+struct PipeCfg {
+  static constexpr int kWaves = 4;
   static constexpr int kThreads = kWaves * 64;
-  static constexpr int kBrickY = 8, kBrickX = 32;
-  static constexpr int kNS = SEG == 16 ? 40 : 64;             // key slots per LDS row
-  static constexpr int kRowTensorBytes = kNS * kRowBytes;     // one key row of K (or V)
-  static constexpr int kStepBytes = 4 * kRowTensorBytes;      // K row0, K row1, V row0, V row1
-  static constexpr int kSmem = NBUF * kStepBytes;
-  static constexpr int kDmaTotal = kNS;                        // 1 KiB DMA copies per step
-  static constexpr int kDmaPerWave = (kDmaTotal + kWaves - 1) / kWaves;  // per wave (last ones repeat)
+  static constexpr int kBrickY = 4, kBrickX = 32;
+  static constexpr int kRows = SEG == 16 ? 2 : 1;        // key rows per step
+  static constexpr int kNS = SEG == 16 ? 40 : 64;        // key slots per LDS row (>= 24 + SEG)
+  static constexpr int kRowL = kNS * kRowBytes;          // one LDS key row
+  static constexpr int kSlot = kRows * kRowL;            // one ring slot: one tensor, one step
+  static constexpr int kK = 0, kV = 2 * kSlot;           // K slots 0,1 then V slots 0,1
+  static constexpr int kSmem = 4 * kSlot;
+  static constexpr int kCopies = kRows * kNS / 4;        // 1 KiB DMA copies per tensor per step
+  static_assert(kCopies % kWaves == 0, "copies split evenly over the waves");
+  static constexpr int kCopiesPerWave = kCopies / kWaves;
 };
 
 __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_row) {
@@ -282,11 +289,12 @@ __device__ __forceinline__ void wait_vmem() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | N);
 }
 
-template <int SEG, int NBUF>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void na3d_rows_kernel(const Na3dArgs a, int n_yb, int n_xb) {
-  using C = RowCfg<SEG, NBUF>;
-  constexpr int RT = C::kRowTensorBytes;
+__device__ __forceinline__ bool is_nan_bits(float x) { return (__float_as_uint(x) & 0x7fffffffu) > 0x7f800000u; }
+
+template <int SEG>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
+  using C = PipeCfg<SEG>;
   __shared__ __attribute__((aligned(16))) unsigned char smem[C::kSmem];
   VX_LDS unsigned char* const lds = (VX_LDS unsigned char*)smem;
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
@@ -319,30 +327,26 @@ void na3d_rows_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   const int T = a.T, Hs = a.Hs, W = a.W, kt = a.kt, kh = a.kh, kw = a.kw;
   const int y0 = yb * C::kBrickY, x0 = xb * C::kBrickX;
 
-  // ---- the workgroup's key rows.
+  // ---- the workgroup's key rows (box rows r = tr * NY + yr).
   const int t_lo = window_start(t, T, kt);
   const int Y_lo = window_start(y0, Hs, kh);
   const int NY = window_start(min(y0 + C::kBrickY - 1, Hs - 1), Hs, kh) + kh - Y_lo;
   const int X_lo = window_start(x0, W, kw);
   const int nrows = kt * NY;
-  const int n_steps = (nrows + 1) / 2;
+  const int n_steps = (nrows + C::kRows - 1) / C::kRows;
 
-  // ---- this wave's queries: y rows yq0..yq0+3, x columns xq0..xq0+7.
-  const int yq0 = y0 + 4 * (wave >> 2);
-  const int xq0 = x0 + 8 * (wave & 3);
-  const bool wave_live = yq0 < Hs && xq0 < W;
-  const int yw_lo = window_start(min(yq0, Hs - 1), Hs, kh) - Y_lo;          // wave's y window, in
-  const int yw_hi = window_start(min(yq0 + 3, Hs - 1), Hs, kh) + kh - Y_lo;  // box rows
-  const int ox = window_start(min(xq0, W - 1), W, kw) - X_lo;  // wave's first x slot
+  // ---- this wave's queries: y rows y0..y0+3, x columns xq0..xq0+7.
+  const int xq0 = x0 + 8 * wave;
+  const int ox = window_start(min(xq0, W - 1), W, kw) - X_lo;  // wave's first x slot, <= 24
 
   // ---- this lane's query and its window.
-  const int yq = yq0 + col / 8, xq = xq0 + col % 8;
+  const int yq = y0 + col / 8, xq = xq0 + col % 8;
   const bool q_in = yq < Hs && xq < W;
   const int yqc = min(yq, Hs - 1), xqc = min(xq, W - 1);
   const int sy = window_start(yqc, Hs, kh) - Y_lo;
   const int sx = window_start(xqc, W, kw) - X_lo - ox;  // in [0, SEG - kw]
-  // Per score register i: +inf if its key's x slot lies in this lane's
-  // window, -inf otherwise (the mask is a v_min3 with the row limit below).
+  // Per score register i (key (i/4)*8 + hf*4 + i%4 of the chunk): +inf if
+  // its x slot lies in this lane's window, -inf otherwise.
   float xlim[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -365,49 +369,60 @@ void na3d_rows_kernel(const Na3dArgs a, int n_yb, int n_xb) {
     for (int ds = 0; ds < 8; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
   }
 
-  // ---- DMA of step s into ring slot s % NBUF: copy i of the step covers
-  // tensor i / (kNS/2), row i / (kNS/4) % 2 and x slots 4*(i % (kNS/4)) + 0..3.
-  // The lane-dependent part of every copy's source address (x position and
-  // swizzled 16-byte chunk) is fixed for the workgroup; only the row token
-  // changes per step and is computed once per step in scalar registers.
+  // ---- DMA of one step of one tensor: copy i covers LDS row i / (kNS/4) of
+  // the slot and key slots 4*(i % (kNS/4)) + 0..3; wave w issues copies
+  // w, w + 4, ... The lane-dependent part of each copy's source (x position,
+  // swizzled 16-byte chunk) is fixed for the workgroup; the row tokens change
+  // per step and are scalar.
   const int srow = lane >> 4, scol = lane & 15;
-  int64_t dma_off[C::kDmaPerWave];
+  int64_t dma_off[C::kCopiesPerWave];
+  int dma_dst[C::kCopiesPerWave], dma_row[C::kCopiesPerWave];
 #pragma unroll
-  for (int p = 0; p < C::kDmaPerWave; ++p) {
-    // copies past kDmaTotal repeat the last one (same bytes, same place), so
-    // every wave issues the same number of copies per step
-    const int i = min(wave * C::kDmaPerWave + p, C::kDmaTotal - 1);
-    const int pos = 4 * (i % (C::kNS / 4)) + srow;
+  for (int p = 0; p < C::kCopiesPerWave; ++p) {
+    const int i = wave + C::kWaves * p;
+    const int g = i % (C::kNS / 4);
+    const int pos = 4 * g + srow;
+    dma_row[p] = i / (C::kNS / 4);
+    dma_dst[p] = dma_row[p] * C::kRowL + 4 * g * kRowBytes;
     dma_off[p] = (int64_t)min(X_lo + pos, W - 1) * tok_stride + ((scol ^ row_swizzle(pos)) * 8);
   }
-  // (t', y') of box row r as a token offset, and its y index within the box.
-  auto row_token = [&](int r, int& yr) -> int64_t {
-    const int tr = r / NY;
-    yr = r - tr * NY;
-    return (((int64_t)(t_lo + tr) * Hs + (Y_lo + yr)) * W) * tok_stride;
+  // Box rows are walked with cursors (row index, its y in the box, its token
+  // offset) that advance one row at a time and stop at the last row, so no
+  // step divides by NY.
+  struct Cursor {
+    int r, yr;
+    int64_t tok;
   };
-  auto issue_step = [&](int s) {
-    const int slot = s % NBUF;
-    int yr_unused;
-    const int64_t rt0 = row_token(min(2 * s, nrows - 1), yr_unused);
-    const int64_t rt1 = row_token(min(2 * s + 1, nrows - 1), yr_unused);
-#pragma unroll
-    for (int p = 0; p < C::kDmaPerWave; ++p) {
-      const int i = min(wave * C::kDmaPerWave + p, C::kDmaTotal - 1);
-      const int tensor = i / (C::kNS / 2);
-      const int rowsel = (i / (C::kNS / 4)) & 1;
-      const int g = i % (C::kNS / 4);
-      const bf16* src = (tensor ? vg : kg) + (rowsel ? rt1 : rt0) + dma_off[p];
-      const int dst = slot * C::kStepBytes + (2 * tensor + rowsel) * RT + 4 * g * kRowBytes;
-      lds_dma16(src, lds_base + dst);
+  const int64_t row_step = (int64_t)W * tok_stride;             // next y
+  const int64_t plane_jump = (int64_t)(Hs - NY) * W * tok_stride;  // last y of a plane -> first y of the next
+  auto advance = [&](Cursor& c) {
+    if (c.r + 1 < nrows) {
+      ++c.r;
+      c.tok += row_step;
+      if (++c.yr == NY) {
+        c.yr = 0;
+        c.tok += plane_jump;
+      }
     }
   };
+  const Cursor first = {0, 0, ((int64_t)t_lo * Hs + Y_lo) * W * tok_stride};
+  // Issues the copies of one step (rows c, c+1) and moves c on by kRows rows.
+  auto issue = [&](const bf16* base, int slot_off, Cursor& c) {
+    const int64_t rt0 = c.tok;
+    advance(c);
+    const int64_t rt1 = C::kRows == 2 ? c.tok : rt0;
+    if (C::kRows == 2) advance(c);
+#pragma unroll
+    for (int p = 0; p < C::kCopiesPerWave; ++p)
+      lds_dma16(base + (dma_row[p] ? rt1 : rt0) + dma_off[p], lds_base + slot_off + dma_dst[p]);
+  };
 
-  // ---- per-lane LDS offsets. K fragment: key col of the chunk.
+  // ---- per-lane LDS offsets. K fragment: key col of the chunk (SEG = 16:
+  // keys 0-15 from the step's first row, 16-31 from its second).
   int kbase, ksw;
   if (SEG == 16) {
     const int pos = ox + (col & 15);
-    kbase = (col >> 4) * RT + pos * kRowBytes;
+    kbase = (col >> 4) * C::kRowL + pos * kRowBytes;
     ksw = row_swizzle(pos);
   } else {
     const int pos = ox + col;
@@ -427,99 +442,147 @@ void na3d_rows_kernel(const Na3dArgs a, int n_yb, int n_xb) {
     const int sw = row_swizzle(pos);
 #pragma unroll
     for (int db1 = 0; db1 < 2; ++db1)
-      voff[e][db1] = 2 * RT + pos * kRowBytes + (((4 * db1 + 2 * dh + (vc >> 1)) ^ sw) * 16) + (vc & 1) * 8;
+      voff[e][db1] = pos * kRowBytes + (((4 * db1 + 2 * dh + (vc >> 1)) ^ sw) * 16) + (vc & 1) * 8;
   }
+  auto vfrag = [&](const VX_LDS unsigned char* vb, int j, int db) -> bf16x8 {
+    const int jo = SEG == 16 ? j * C::kRowL : j * 16 * kRowBytes;
+    const VX_LDS unsigned char* p0 = vb + jo + voff[0][db & 1] + (db >> 1) * 128;
+    const VX_LDS unsigned char* p1 = vb + jo + voff[1][db & 1] + (db >> 1) * 128;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p0);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p1);
+    return concat(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi));
+  };
+  auto kfrag = [&](const VX_LDS unsigned char* kb, int ds) -> bf16x8 {
+    return *(const VX_LDS bf16x8*)(kb + koff[ds & 3] + (ds >> 2) * 128);
+  };
 
   f32x16 O[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) O[db] = f32x16{};
   float m_run = kNegBig, l_run = 0.f;
   const float c2 = a.scale * kLog2e;
+  const bf16x2 one2 = {(bf16)1.0f, (bf16)1.0f};
 
-  // One 32-key chunk: K rows at kaddr + koff, V rows at vaddr + voff; rows
-  // r0 (keys 0-15) and r1 (keys 16-31) of the box, x slots from this
-  // wave's window (SEG = 16), or one row r0 for all 32 keys (SEG = 32).
-  // ok0/ok1: the chunk's first / second 16 keys come from an existing box
-  // row; yr0/yr1: those rows' y index within the box.
-  auto chunk = [&](const VX_LDS unsigned char* kaddr, const VX_LDS unsigned char* vaddr, bool ok0, int yr0,
-                   bool ok1, int yr1) {
-    f32x16 S = f32x16{};
+  // ---- prologue: K of steps 0 and 1 in flight, V slot 1 zeroed (it stands
+  // in for the V of step -1, paired with P = 0), S = QK^T of chunk 0.
+  Cursor kcur = first;  // rows of the next K step to issue
+  Cursor vcur = first;  // rows of the next V step to issue (and of the chunk being masked)
+  issue(kg, C::kK, kcur);
+  issue(kg, C::kK + C::kSlot, kcur);
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) {
-      const bf16x8 kf = *(const VX_LDS bf16x8*)(kaddr + koff[ds & 3] + (ds >> 2) * 128);
-      S = mfma32x32x16(kf, qr[ds], S);
-    }
-    // window mask: keys outside this lane's y or x window -> -inf
+  for (int p = 0; p < C::kSlot / (C::kThreads * 16); ++p)
+    *(VX_LDS u32x4*)(lds + C::kV + C::kSlot + (p * C::kThreads + threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
+  wait_vmem<0>();
+  __syncthreads();
+  f32x16 S = f32x16{};
+#pragma unroll
+  for (int ds = 0; ds < 8; ++ds) S = mfma32x32x16(kfrag(lds + C::kK, ds), qr[ds], S);
+  bf16x8 Pp[2] = {bf16x8{}, bf16x8{}};
+
+  // One step: consumes S (scores of chunk s) and Pp (probabilities of chunk
+  // s-1), produces Sn (scores of chunk s+1) and P (probabilities of chunk s).
+  auto step = [&](const int s, f32x16& S, f32x16& Sn, const bf16x8 (&Pp)[2], bf16x8 (&P)[2]) {
+    // The previous step's copies (K of s+1, V of s-1) have landed once this
+    // wave has none outstanding; the barrier publishes everyone's and frees
+    // K slot s%2 (K of s, read last step) and V slot s%2 (V of s-2).
+    wait_vmem<0>();
+    __syncthreads();
+    // window mask of chunk s: keys outside this lane's y window (per row) or
+    // x window (per register) -> -inf
     float rlim[2];
+    {
+      Cursor c = vcur;
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-      const int yr = h2 == 0 ? yr0 : yr1;
-      const bool row_ok = (h2 == 0 ? ok0 : ok1) && (unsigned)(yr - sy) < (unsigned)kh;
-      rlim[h2] = row_ok ? __builtin_inff() : -__builtin_inff();
+      for (int h2 = 0; h2 < 2; ++h2) {
+        if (SEG == 16 && h2 == 1) advance(c);
+        const int r = s * C::kRows + (SEG == 16 ? h2 : 0);
+        const bool row_ok = r < nrows && (unsigned)(c.yr - sy) < (unsigned)kh;
+        rlim[h2] = row_ok ? __builtin_inff() : -__builtin_inff();
+      }
+    }
+    issue(kg, C::kK + (s & 1) * C::kSlot, kcur);
+    issue(vg, C::kV + (s & 1) * C::kSlot, vcur);
+
+    const VX_LDS unsigned char* kb = lds + C::kK + ((s + 1) & 1) * C::kSlot;  // K of chunk s+1
+    const VX_LDS unsigned char* vb = lds + C::kV + ((s + 1) & 1) * C::kSlot;  // V of chunk s-1
+    auto frag = [&](int i) -> bf16x8 { return i < 8 ? vfrag(vb, i >> 2, i & 3) : kfrag(kb, i - 8); };
+    Sn = f32x16{};
+    float l_tile = 0.f;
+    const float mneg = -m_run;
+    bf16x8 fr[16];
+    float pf[16];
+    bf16x2 pk[8];
+    fr[0] = frag(0);
+    fr[1] = frag(1);
+    // 16 slots: slot i issues one MFMA (i < 8: PV(s-1), i >= 8: QK^T(s+1)),
+    // the LDS read two slots ahead, and the mask + exp of score i of chunk s.
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i + 2 < 16) fr[i + 2] = frag(i + 2);
+      if (i < 8)
+        O[i & 3] = mfma32x32x16(fr[i], Pp[i >> 2], O[i & 3]);
+      else
+        Sn = mfma32x32x16(fr[i], qr[i - 8], Sn);
+      S[i] = __builtin_fminf(__builtin_fminf(S[i], xlim[i]), rlim[i >> 3]);
+      pf[i] = fast_exp2(__builtin_fmaf(S[i], c2, mneg));
+      if (i & 1) {
+        pk[i >> 1] = bf16x2{(bf16)pf[i - 1], (bf16)pf[i]};
+        l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[i >> 1], one2, l_tile, false);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) S[i] = __builtin_fminf(__builtin_fminf(S[i], xlim[i]), rlim[i >> 3]);
-    float mx = S[0];
+    for (int j = 0; j < 2; ++j)
+      P[j] = __builtin_shufflevector(__builtin_shufflevector(pk[4 * j], pk[4 * j + 1], 0, 1, 2, 3),
+                                     __builtin_shufflevector(pk[4 * j + 2], pk[4 * j + 3], 0, 1, 2, 3),
+                                     0, 1, 2, 3, 4, 5, 6, 7);
+    // rare: a probability may exceed 2^kRescaleSlack (the lane's chunk sum is
+    // above kSumLimit, inf or NaN; the first chunk with a key in the window
+    // always lands here) -> raise m_run to the chunk max, rescale O and l and
+    // recompute the chunk's probabilities.
+    if (__builtin_amdgcn_ballot_w64(l_tile > kSumLimit || is_nan_bits(l_tile)) != 0) {
+      float mx = S[0];
 #pragma unroll
-    for (int i = 1; i < 16; ++i) mx = __builtin_fmaxf(mx, S[i]);
-    const float ms = halves_max(mx) * c2;  // scores stay raw; c2 folds into the exp argument
-    if (__builtin_amdgcn_ballot_w64(ms > m_run + kRescaleSlack) != 0) {
-      const float mn = __builtin_fmaxf(m_run, ms);
+      for (int i = 1; i < 16; ++i) mx = __builtin_fmaxf(mx, S[i]);
+      const float mn = __builtin_fmaxf(m_run, halves_max(mx) * c2);
       const float alpha = fast_exp2(m_run - mn);
       m_run = mn;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < 4; ++db) O[db] *= alpha;
-    }
-    bf16x8 P[2];
+      l_tile = 0.f;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      bf16x8 pv;
-      const float mneg = -m_run;
+      for (int j = 0; j < 2; ++j) {
+        bf16x8 pv;
 #pragma unroll
-      for (int r = 0; r < 8; ++r) pv[r] = (bf16)fast_exp2(__builtin_fmaf(S[8 * j + r], c2, mneg));
-      P[j] = pv;
-      l_run = sum8(pv, l_run);
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const int jo = SEG == 16 ? j * RT : j * 16 * kRowBytes;
-        const VX_LDS unsigned char* p0 = vaddr + jo + voff[0][db & 1] + (db >> 1) * 128;
-        const VX_LDS unsigned char* p1 = vaddr + jo + voff[1][db & 1] + (db >> 1) * 128;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p0);
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p1);
-        const bf16x8 vf = concat(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi));
-        O[db] = mfma32x32x16(vf, P[j], O[db]);
+        for (int r = 0; r < 8; ++r) pv[r] = (bf16)fast_exp2(__builtin_fmaf(S[8 * j + r], c2, -mn));
+        P[j] = pv;
+        l_tile = sum8(pv, l_tile);
       }
+    }
+    l_run += l_tile;
   };
 
-  // ---- prologue: the first NBUF-1 steps in flight.
-#pragma unroll
-  for (int s = 0; s < NBUF - 1; ++s) issue_step(min(s, n_steps - 1));
-  for (int s = 0; s < n_steps; ++s) {
-    // Step s landed once only the NBUF-2 most recent steps may be in flight.
-    wait_vmem<C::kDmaPerWave * (NBUF - 2)>();
-    __syncthreads();
-    // The slot of step s-1 is free now: refill it with step s+NBUF-1.
-    issue_step(min(s + NBUF - 1, n_steps - 1));
-    int y0r, y1r;
-    (void)row_token(2 * s, y0r);
-    (void)row_token(min(2 * s + 1, nrows - 1), y1r);
-    const bool ok1 = 2 * s + 1 < nrows;
-    const bool live = wave_live && ((y0r >= yw_lo && y0r < yw_hi) || (ok1 && y1r >= yw_lo && y1r < yw_hi));
-    if (live) {
-      const VX_LDS unsigned char* base = lds + (s % NBUF) * C::kStepBytes;
-      if (SEG == 16) {
-        chunk(base, base, true, y0r, ok1, y1r);
-      } else {
-        chunk(base, base, true, y0r, true, y0r);
-        chunk(base + RT, base + RT, ok1, y1r, ok1, y1r);
-      }
-    }
+  f32x16 S2;
+  bf16x8 P2[2];
+  int s = 0;
+  for (; s + 1 < n_steps; s += 2) {
+    step(s, S, S2, Pp, P2);
+    step(s + 1, S2, S, P2, Pp);
   }
+  if (s < n_steps) {
+    step(s, S, S2, Pp, P2);
+    Pp[0] = P2[0];
+    Pp[1] = P2[1];
+  }
+  // ---- PV of the last chunk (its V was issued by the last step).
   wait_vmem<0>();
+  __syncthreads();
+  {
+    const VX_LDS unsigned char* vb = lds + C::kV + ((n_steps - 1) & 1) * C::kSlot;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) O[i & 3] = mfma32x32x16(vfrag(vb, i >> 2, i & 3), Pp[i >> 2], O[i & 3]);
+  }
 
   const float lt = halves_sum(l_run);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
@@ -543,13 +606,13 @@ int launch_na3d_fwd(const Na3dArgs& a, void* stream) {
   if (a.D != kD) return (int)hipErrorNotSupported;
   hipStream_t st = (hipStream_t)stream;
   if (a.kw <= 25) {
-    const int n_yb = (a.Hs + 7) / 8;
+    const int n_yb = (a.Hs + 3) / 4;
     const int n_xb = (a.W + 31) / 32;
     dim3 grid((unsigned)a.T * n_yb * n_xb, a.NH, a.B);
     if (a.kw <= 9)
-      hipLaunchKernelGGL((na3d_rows_kernel<16, 4>), grid, dim3(512), 0, st, a, n_yb, n_xb);
+      hipLaunchKernelGGL((na3d_pipe_kernel<16>), grid, dim3(256), 0, st, a, n_yb, n_xb);
     else
-      hipLaunchKernelGGL((na3d_rows_kernel<32, 2>), grid, dim3(512), 0, st, a, n_yb, n_xb);
+      hipLaunchKernelGGL((na3d_pipe_kernel<32>), grid, dim3(256), 0, st, a, n_yb, n_xb);
     return (int)hipGetLastError();
   }
   const int n_yb = (a.Hs + kBrickY - 1) / kBrickY;

@@ -19,13 +19,13 @@ __all__ = ["neighborhood_attention_3d", "na3d_attention", "na3d_kernel_name"]
 
 def na3d_kernel_name(width: int, kernel_w: int) -> str:
     """Name of the kernel the library launches for this x window (profiling aid):
-    the row-streaming kernel with 16- or 32-key x segments up to kw' = 25, the
-    per-wave kernel above that (kw' = min(kw, W))."""
+    the pipelined row-streaming kernel with 16- or 32-key x segments up to
+    kw' = 25, the per-wave kernel above that (kw' = min(kw, W))."""
     kw = min(int(kernel_w), int(width))
     if kw <= 9:
-        return "na3d_rows_kernel<16, 4>"
+        return "na3d_pipe_kernel<16>"
     if kw <= 25:
-        return "na3d_rows_kernel<32, 2>"
+        return "na3d_pipe_kernel<32>"
     return "na3d_wave_kernel"
 
 
