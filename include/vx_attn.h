@@ -55,7 +55,9 @@ const char* vx_last_error(void);
  *   key_bias   float32[B, key_mask_stride] or NULL: added to the logits of
  *              key j after scaling; -inf masks the key (Cosmos3's
  *              (B,1,1,Sk) bias, src/vidax/models/cosmos3/dit_layers.py:124-135).
- * key_mask_stride is in elements, a multiple of 4 and >= round_up(Sk, 4);
+ * key_mask_stride is in elements, a multiple of 4 and >= round_up(Sk, 64) (the
+ * kernel stages whole 64-key tiles of the mask; padding entries are not read
+ * as keys);
  * key_valid must be 4-byte and key_bias 16-byte aligned.
  * A query row whose keys are all masked produces an all-zero output row.
  *

@@ -32,7 +32,7 @@ def test_header_symbols_are_exported():
 
 
 def test_abi_version():
-    assert _lib.lib().vx_abi_version() == 10000
+    assert _lib.lib().vx_abi_version() == 10100
 
 
 def _flash_check(**kw):
@@ -50,8 +50,8 @@ def test_flash_check_accepts_valid_arguments():
     assert _flash_check() == _lib.VX_OK
     assert _lib.last_error() == ""
     assert _flash_check(qs=(200 * 4 * 128, 4 * 128, 128)) == _lib.VX_OK
-    assert _flash_check(key_valid=A, stride=200) == _lib.VX_OK
-    assert _flash_check(key_bias=A, kv_len=A, stride=204) == _lib.VX_OK
+    assert _flash_check(key_valid=A, stride=256) == _lib.VX_OK
+    assert _flash_check(key_bias=A, kv_len=A, stride=260) == _lib.VX_OK
 
 
 @pytest.mark.parametrize("kw,code,frag", [
@@ -66,10 +66,10 @@ def test_flash_check_accepts_valid_arguments():
     (dict(scale=-1.0), _lib.VX_ERR_INVALID_ARGUMENT, "scale"),
     (dict(qs=(0, 4 * 128, 129)), _lib.VX_ERR_INVALID_ARGUMENT, "multiple of 8"),
     (dict(ks=(0, -512, 128)), _lib.VX_ERR_INVALID_ARGUMENT, "negative"),
-    (dict(key_valid=A, stride=199), _lib.VX_ERR_INVALID_ARGUMENT, "key_mask_stride"),
-    (dict(key_valid=A, stride=198), _lib.VX_ERR_INVALID_ARGUMENT, "key_mask_stride"),
-    (dict(key_valid=A + 2, stride=200), _lib.VX_ERR_INVALID_ARGUMENT, "4-byte"),
-    (dict(key_bias=A + 4, stride=200), _lib.VX_ERR_INVALID_ARGUMENT, "16-byte"),
+    (dict(key_valid=A, stride=200), _lib.VX_ERR_INVALID_ARGUMENT, "key_mask_stride"),
+    (dict(key_valid=A, stride=258), _lib.VX_ERR_INVALID_ARGUMENT, "key_mask_stride"),
+    (dict(key_valid=A + 2, stride=256), _lib.VX_ERR_INVALID_ARGUMENT, "4-byte"),
+    (dict(key_bias=A + 4, stride=256), _lib.VX_ERR_INVALID_ARGUMENT, "16-byte"),
 ])
 def test_flash_check_rejects(kw, code, frag):
     assert _flash_check(**kw) == code

@@ -54,9 +54,10 @@ def _aligned(t: torch.Tensor) -> torch.Tensor:
 
 
 def _mask_rows(x: torch.Tensor, sk: int, dtype: torch.dtype, fill) -> torch.Tensor:
-    """(B, Sk) -> (B, round_up(Sk, 4)) contiguous copy in `dtype`, padded with `fill`."""
+    """(B, Sk) -> (B, round_up(Sk, 64)) contiguous copy in `dtype`, padded with `fill`
+    (the kernel stages the mask in whole 64-key tiles)."""
     b = x.shape[0]
-    width = (sk + 3) // 4 * 4
+    width = (sk + 63) // 64 * 64
     out = torch.full((b, width), fill, dtype=dtype, device=x.device)
     out[:, :sk] = x.to(dtype)
     return out

@@ -43,6 +43,14 @@ constexpr int kTileBytes = kBN * kRowBytes;   // 16 KiB
 constexpr int kVBuf = 0;                      // three V tiles
 constexpr int kKBuf = 3 * kTileBytes;         // three K tiles
 constexpr int kSmemBytes = 6 * kTileBytes;    // 96 KiB
+// Key masks of the masked variants go through LDS like K: a ring of 4 slots
+// of 320 bytes (64 validity bytes, then 64 fp32 biases), slot j % 4 holding
+// tile j's mask, staged by wave 0 together with K_j.
+constexpr int kMaskBuf = 6 * kTileBytes;
+constexpr int kMaskSlot = 320;
+constexpr int kMaskRing = 4;
+// Mask kinds (template argument): no mask, validity bytes, additive biases, both.
+constexpr int kMaskNone = 0, kMaskValid = 1, kMaskBias = 2;
 constexpr int kLoadsPerWave = (kBN / 4) / kWaves;  // 1 KiB wave loads per tile
 constexpr float kRescaleSlack = 8.0f;         // log2 units
 constexpr float kSumLimit = 256.0f;           // 2^kRescaleSlack
@@ -79,14 +87,16 @@ __device__ __forceinline__ void wait_vmem() {
 // NaN test on the bit pattern (stays exact when the compiler may assume no NaNs).
 __device__ __forceinline__ bool is_nan_bits(float x) { return (__float_as_uint(x) & 0x7fffffffu) > 0x7f800000u; }
 
-template <bool MASKED>
+template <int MASK>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_fwd_kernel(const FlashArgs a) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[kSmemBytes];
+  constexpr bool MASKED = MASK != kMaskNone;
+  constexpr int kMaskCopies = (MASK & kMaskValid ? 1 : 0) + (MASK & kMaskBias ? 1 : 0);
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kSmemBytes + (MASKED ? kMaskRing * kMaskSlot : 0)];
   lds_u8* const lds = (lds_u8*)smem;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int hf = lane >> 5;   // which half of the wave
   const int col = lane & 31;  // query column within the wave's 32
   const int b = blockIdx.z;
@@ -217,14 +227,39 @@ void flash_fwd_kernel(const FlashArgs a) {
   for (int db = 0; db < 4; ++db) O[db] = f32x16{};
   float m_run = kNegBig, l_run = 0.f;
 
-  const uint8_t* vrow = (MASKED && a.key_valid) ? a.key_valid + (int64_t)b * a.key_mask_stride : nullptr;
-  const float* brow = (MASKED && a.key_bias) ? a.key_bias + (int64_t)b * a.key_mask_stride : nullptr;
+  const uint8_t* vrow = (MASK & kMaskValid) ? a.key_valid + (int64_t)b * a.key_mask_stride : nullptr;
+  const float* brow = (MASK & kMaskBias) ? a.key_bias + (int64_t)b * a.key_mask_stride : nullptr;
+  // Wave 0 stages tile j's mask (64 validity bytes: lanes 0-3; 64 biases:
+  // lanes 0-15) into mask slot j % 4. Mask rows hold whole 64-key tiles.
+  auto stage_mask = [&](int j) {
+    if (!MASKED || wave != 0) return;
+    const uint32_t slot = lds_base + kMaskBuf + (j & (kMaskRing - 1)) * kMaskSlot;
+    if (MASK & kMaskValid) {
+      if (lane < 4) lds_dma16(vrow + j * kBN + lane * 16, slot);
+    }
+    if (MASK & kMaskBias) {
+      if (lane < 16) lds_dma16(brow + j * kBN + lane * 4, slot + 64);
+    }
+  };
+  // This wave's DMA instructions of one iteration: the previous iteration's
+  // may still be in flight at the top of the next one.
+  auto wait_prev = [&]() {
+    if (MASKED && wave == 0)
+      wait_vmem<2 * kLoadsPerWave + kMaskCopies>();
+    else
+      wait_vmem<2 * kLoadsPerWave>();
+  };
 
   if (n_tiles > 0) {
     // Tile j of K lives in K buffer j % 3 and tile j of V in V buffer j % 3;
     // V buffer 2 stands in for "V_{-1}" (zeros, paired with P = 0 in
     // iteration 0). Iteration t issues K_{t+3} and V_{t+1}, two iterations
     // before they are read, so their latency is hidden.
+    // masks of tiles 0-2 first: they are older than every copy the first
+    // iterations wait for
+    stage_mask(0);
+    stage_mask(min(1, n_tiles - 1));
+    stage_mask(min(2, n_tiles - 1));
     stage(kg, klane, a.ks[1], 0, kKBuf);
     stage(kg, klane, a.ks[1], min(1, n_tiles - 1), kKBuf + kTileBytes);
     stage(kg, klane, a.ks[1], min(2, n_tiles - 1), kKBuf + 2 * kTileBytes);
@@ -255,7 +290,7 @@ void flash_fwd_kernel(const FlashArgs a) {
       // still be outstanding; the barrier then publishes them, and it also
       // frees K buffer t % 3 (K_t, read by QK(t) last iteration) and V buffer
       // (t+1) % 3 (V_{t-2}) for this iteration's prefetch.
-      wait_vmem<2 * kLoadsPerWave>();
+      wait_prev();
       __syncthreads();
       const int kb_next = kb_cur == 0 ? 2 : kb_cur - 1;  // t % 3
       const int vb_next = vb_prev == 2 ? 1 : (vb_prev == 1 ? 0 : 2);  // (t+1) % 3
@@ -265,26 +300,24 @@ void flash_fwd_kernel(const FlashArgs a) {
       // masked keys -> -inf, and use cc = 1 below; fully valid tiles keep the
       // fused scale in the exp argument.
       const int key0 = t * kBN;
-      const int klast = (kv_end - 1) & ~3;  // last aligned 4-key group inside the loop
+      const lds_u8* mslot = lds + kMaskBuf + (t & (kMaskRing - 1)) * kMaskSlot;  // tile t's mask
       uint32_t vbits[2][4];
       bool slow = key0 + kBN > kv_end;
-      if (MASKED) {
-        if (vrow != nullptr) {
-          bool hole = false;
+      if (MASK & kMaskValid) {
+        bool hole = false;
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const int kbase = key0 + kb * 32 + g * 8 + hf * 4;  // multiple of 4
-              vbits[kb][g] = *(const uint32_t*)(vrow + min(kbase, klast));
-              // a zero byte anywhere in the word marks an invalid key
-              hole |= ((vbits[kb][g] - 0x01010101u) & ~vbits[kb][g] & 0x80808080u) != 0;
-            }
-          slow = slow || __builtin_amdgcn_ballot_w64(hole) != 0;
-        }
-        slow = slow || brow != nullptr;
+          for (int g = 0; g < 4; ++g) {
+            vbits[kb][g] = *(const VX_LDS uint32_t*)(mslot + kb * 32 + g * 8 + hf * 4);
+            // a zero byte anywhere in the word marks an invalid key
+            hole |= ((vbits[kb][g] - 0x01010101u) & ~vbits[kb][g] & 0x80808080u) != 0;
+          }
+        slow = slow || __builtin_amdgcn_ballot_w64(hole) != 0;
       }
+      if (MASK & kMaskBias) slow = true;
       stage(kg, klane, a.ks[1], min(t + 3, n_tiles - 1), kKBuf + kb_next * kTileBytes);
+      stage_mask(min(t + 3, n_tiles - 1));
       stage(vg, vlane, a.vs[1], min(t + 1, n_tiles - 1), kVBuf + vb_next * kTileBytes);
       float cc = c;
       if (slow) {
@@ -295,11 +328,11 @@ void flash_fwd_kernel(const FlashArgs a) {
           for (int g = 0; g < 4; ++g) {
             const int kbase = key0 + kb * 32 + g * 8 + hf * 4;
             f32x4 bias = {0.f, 0.f, 0.f, 0.f};
-            if (MASKED && brow != nullptr) bias = *(const f32x4*)(brow + min(kbase, klast)) * kLog2e;
+            if (MASK & kMaskBias) bias = *(const VX_LDS f32x4*)(mslot + 64 + (kbase - key0) * 4) * kLog2e;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               bool ok = kbase + e < kv_end;
-              if (MASKED && vrow != nullptr) ok = ok && ((vbits[kb][g] >> (8 * e)) & 0xffu) != 0;
+              if (MASK & kMaskValid) ok = ok && ((vbits[kb][g] >> (8 * e)) & 0xffu) != 0;
               const float sv = __builtin_fmaf(S[kb][g * 4 + e], c, bias[e]);
               S[kb][g * 4 + e] = ok ? sv : -__builtin_inff();
             }
@@ -423,10 +456,10 @@ void flash_fwd_kernel(const FlashArgs a) {
   }
 }
 
-template <bool MASKED>
+template <int MASK>
 int launch(const FlashArgs& a, hipStream_t stream) {
   dim3 grid((a.Sq + kQueriesPerBlock - 1) / kQueriesPerBlock, a.H, a.B);
-  hipLaunchKernelGGL((flash_fwd_kernel<MASKED>), grid, dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL((flash_fwd_kernel<MASK>), grid, dim3(kThreads), 0, stream, a);
   return (int)hipGetLastError();
 }
 
@@ -434,8 +467,13 @@ int launch(const FlashArgs& a, hipStream_t stream) {
 
 int launch_flash_fwd(const FlashArgs& a, void* stream) {
   hipStream_t s = (hipStream_t)stream;
-  if (a.key_valid != nullptr || a.key_bias != nullptr) return launch<true>(a, s);
-  return launch<false>(a, s);
+  const int mask = (a.key_valid != nullptr ? kMaskValid : 0) | (a.key_bias != nullptr ? kMaskBias : 0);
+  switch (mask) {
+    case kMaskValid: return launch<kMaskValid>(a, s);
+    case kMaskBias: return launch<kMaskBias>(a, s);
+    case kMaskValid | kMaskBias: return launch<kMaskValid | kMaskBias>(a, s);
+    default: return launch<kMaskNone>(a, s);
+  }
 }
 
 }  // namespace vx

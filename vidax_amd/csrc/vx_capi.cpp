@@ -76,10 +76,10 @@ int32_t flash_check(const void* q, const void* k, const void* v, const void* out
   if (!(scale > 0.f) || !std::isfinite(scale))
     return fail(VX_ERR_INVALID_ARGUMENT, "scale must be positive and finite (got %g)", (double)scale);
   if (key_valid != nullptr || key_bias != nullptr) {
-    const int64_t need = ((int64_t)Sk + 3) / 4 * 4;
+    const int64_t need = ((int64_t)Sk + 63) / 64 * 64;
     if (key_mask_stride < need || key_mask_stride % 4 != 0)
       return fail(VX_ERR_INVALID_ARGUMENT,
-                  "key_mask_stride (%lld) must be a multiple of 4 and >= round_up(seq_k, 4) = %lld",
+                  "key_mask_stride (%lld) must be a multiple of 4 and >= round_up(seq_k, 64) = %lld",
                   (long long)key_mask_stride, (long long)need);
     if (key_valid != nullptr && (reinterpret_cast<uintptr_t>(key_valid) & 3u) != 0)
       return fail(VX_ERR_INVALID_ARGUMENT, "key_valid must be 4-byte aligned");
@@ -174,7 +174,7 @@ int32_t injected() {
 
 extern "C" {
 
-int32_t vx_abi_version(void) { return 10000; }
+int32_t vx_abi_version(void) { return 10100; }
 
 const char* vx_last_error(void) { return g_error; }
 
