@@ -38,6 +38,8 @@ WORKLOADS = {
                           "joint self-attention B=1 H=24 S=33*45*80+256, last 0-200 keys masked"),
     "na3d_21x45x80_H24": ("na3d", dict(B=1, T=21, Hs=45, W=80, NH=24, kernel=(3, 7, 7), seed=3),
                           "3D neighbourhood attention 21x45x80, window (3,7,7), B=1 NH=24 D=128"),
+    "qk_norm_rope_L32760_H40": ("prologue", dict(B=1, grid=(21, 30, 52), H=40, seed=5),
+                                "q and k RMSNorm(5120) + 3D RoPE, B=1 L=32760 (21x30x52) H=40 D=128"),
 }
 DEFAULT_WORKLOAD = "self_L32760_H40"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
@@ -121,6 +123,22 @@ def _cpu_baseline(kind, p, budget_s=12.0):
                   f"{Sk} keys, D=128) of this workload, {el:.1f} s")
         return {"value": round(flops / el / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads),
                 "kind": "port", "sample": sample}
+    if kind == "prologue":
+        from oracle import prologue_oracle as P
+        S, L = 2048, p["H"] * 128
+        x = O.bf16_round(rng.standard_normal((1, S, L), dtype=np.float32))
+        w = np.ones(L, np.float32)
+        cos, sin = P.create_rope3d_freqs(1, 32, 64, 128)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            P.qk_norm_rope(x, w, cos, sin, p["H"])
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or reps >= 1000:
+                break
+        gbs = 2.0 * 2 * S * L * reps / el / 1e9
+        sample = f"oracle fp32 (numpy) RMSNorm+RoPE of {S} tokens x {L}, {reps} reps, {el:.1f} s"
+        return {"value": round(gbs, 3), "unit": "GB/s", "cores": int(threads), "kind": "port", "sample": sample}
     # na3d: a slab of T rows with the full H x W plane, all heads
     T = min(3, p["T"])
     shape = (1, T, p["Hs"], p["W"], 2, 128)
@@ -205,6 +223,25 @@ def main(argv=None):
         def step():
             vidax_amd.flash_attention(q, k, v, out=out, **kw)
         kernel_name = "flash_fwd_kernel<true>" if kw else "flash_fwd_kernel<false>"
+    elif kind == "prologue":
+        from vidax_amd.prologue import create_rope3d_freqs, qk_norm_rope
+        g = torch.Generator(device=dev)
+        g.manual_seed(p["seed"])
+        S = p["grid"][0] * p["grid"][1] * p["grid"][2]
+        L = p["H"] * 128
+        qx = torch.randn((p["B"], S, L), generator=g, device=dev).to(torch.bfloat16)
+        kx = torch.randn((p["B"], S, L), generator=g, device=dev).to(torch.bfloat16)
+        wq = 1.0 + 0.1 * torch.randn(L, generator=g, device=dev)
+        wk = 1.0 + 0.1 * torch.randn(L, generator=g, device=dev)
+        freqs = create_rope3d_freqs(*p["grid"], 128, device=dev)
+        flops = 0.0
+        # read and write q and k once (bf16) plus the cos/sin tables once per tensor
+        bytes_ = 2.0 * (2 * 2 * p["B"] * S * L) + 2.0 * (2 * S * 64 * 4)
+
+        def step():
+            qk_norm_rope(qx, wq, freqs, p["H"])
+            qk_norm_rope(kx, wk, freqs, p["H"])
+        kernel_name = "qk_prologue_kernel<16>"
     else:
         g = torch.Generator(device=dev)
         g.manual_seed(p["seed"])
@@ -236,7 +273,12 @@ def main(argv=None):
     ms = sum(per) / len(per)
     tflops = flops / (ms * 1e-3) / 1e12
     gbs = bytes_ / (ms * 1e-3) / 1e9
-    if kind == "flash":
+    if kind == "prologue":
+        tflops = 0.0
+        roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                    "traffic": _traffic(kernel_name, args.workload)}
+    elif kind == "flash":
         roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                     "traffic": _traffic(kernel_name, args.workload)}
@@ -247,10 +289,13 @@ def main(argv=None):
     cpu = None
     if not args.no_cpu_baseline:
         cpu = _cpu_baseline(kind, p, args.cpu_budget)
+    value, unit = round(tflops, 2), "TFLOP/s"
+    if kind == "prologue":
+        value, unit = round(gbs, 1), "GB/s"
     rec = {
         "metric": METRIC,
-        "value": round(tflops, 2),
-        "unit": "TFLOP/s",
+        "value": value,
+        "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,

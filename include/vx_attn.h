@@ -120,6 +120,45 @@ int32_t vx_na3d_check(const void* q, const void* k, const void* v, const void* o
                       float scale);
 
 /*
+ * Fused attention prologue: RMSNorm and/or 3D rotary embedding of q or k in
+ * one pass (read x once, write out once), bf16 in and out. For each token row
+ * (num_heads * head_dim values, contiguous):
+ *   if weight != NULL:  y = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * bf16(weight))
+ *                       with the mean over the whole row (per_head_norm = 0,
+ *                       Wan's q/k norm over the projected dim) or over each
+ *                       head (per_head_norm = 1); fp32 statistics; weight is
+ *                       fp32[num_heads * head_dim]
+ *   else                y = x
+ *   if rope_cos != NULL: every head's adjacent pairs (y[2j], y[2j+1]) are
+ *                       rotated by (rope_cos[s*rope_stride + j],
+ *                       rope_sin[s*rope_stride + j]) in fp32 and rounded to bf16
+ * Output rows have the same (B, S, H, D) layout as the input.
+ *
+ * Replaces the reference's q/k prologue of the DiT attention:
+ *   - src/vidax/core/attention.py:149-161 (RMSNorm: fp32 normalise, cast,
+ *     times the cast scale)
+ *   - src/vidax/core/rope3d.py:88-111 (apply_rope3d: adjacent-pair rotation in
+ *     fp32, cast back), with tables from rope3d.py:45-86 (create_rope3d_freqs)
+ *   - their use in src/vidax/models/wan/common/dit_layers.py:135-149
+ *
+ * Strides {batch, seq} are in elements (NULL = contiguous rows of
+ * num_heads * head_dim), non-negative multiples of 8; x, out, weight and the
+ * tables 16-byte aligned; rope_stride a multiple of 4, >= head_dim / 2.
+ * out may equal x (in place) when the strides are the same.
+ * Supported: head_dim 64 or 128, num_heads * head_dim <= 8192.
+ */
+int32_t vx_rmsnorm_rope_fwd(const void* x, void* out, const float* weight, float eps, int32_t per_head_norm,
+                            const float* rope_cos, const float* rope_sin, int64_t rope_stride, int32_t batch,
+                            int32_t seq, int32_t num_heads, int32_t head_dim, const int64_t* x_strides,
+                            const int64_t* out_strides, void* stream);
+
+/* Host-only argument check for vx_rmsnorm_rope_fwd (no GPU needed). */
+int32_t vx_rmsnorm_rope_check(const void* x, const void* out, const float* weight, float eps, int32_t per_head_norm,
+                              const float* rope_cos, const float* rope_sin, int64_t rope_stride, int32_t batch,
+                              int32_t seq, int32_t num_heads, int32_t head_dim, const int64_t* x_strides,
+                              const int64_t* out_strides);
+
+/*
  * Failure injection for error-path tests: while `code` is non-zero, every
  * vx_*_fwd call that passes argument checks returns `code` without launching,
  * with a message naming the injection. 0 turns it off. Process-wide.

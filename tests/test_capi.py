@@ -32,7 +32,7 @@ def test_header_symbols_are_exported():
 
 
 def test_abi_version():
-    assert _lib.lib().vx_abi_version() == 10100
+    assert _lib.lib().vx_abi_version() == 10200
 
 
 def _flash_check(**kw):
@@ -154,3 +154,44 @@ def test_raise_for_maps_codes():
     _flash_check(B=0)
     with pytest.raises(ValueError):
         _lib.raise_for(_lib.VX_ERR_INVALID_ARGUMENT)
+
+
+def _prologue_check(**kw):
+    args = dict(x=A, out=A + 4096, w=A, eps=1e-6, per_head=0, cos=A, sin=A, tab=64, B=1, S=10, H=4, D=128,
+                xs=None, os_=None)
+    args.update(kw)
+    s2 = lambda s: None if s is None else _lib.strides2(s)
+    return _lib.lib().vx_rmsnorm_rope_check(
+        args["x"], args["out"], args["w"], ctypes.c_float(args["eps"]), args["per_head"], args["cos"],
+        args["sin"], args["tab"], args["B"], args["S"], args["H"], args["D"], s2(args["xs"]), s2(args["os_"]))
+
+
+def test_prologue_check_accepts_valid_arguments():
+    assert _prologue_check() == _lib.VX_OK
+    assert _prologue_check(w=None, per_head=1) == _lib.VX_OK
+    assert _prologue_check(cos=None, sin=None, tab=0) == _lib.VX_OK
+    assert _prologue_check(D=64, tab=32) == _lib.VX_OK
+    assert _prologue_check(H=64) == _lib.VX_OK                              # rows of 8192
+    assert _prologue_check(xs=(10 * 1536, 1536)) == _lib.VX_OK            # q slice of a fused qkv
+    assert _prologue_check(out=A) == _lib.VX_OK                             # in place
+
+
+@pytest.mark.parametrize("kw,code,frag", [
+    (dict(x=None), _lib.VX_ERR_INVALID_ARGUMENT, "non-NULL"),
+    (dict(out=A + 8), _lib.VX_ERR_INVALID_ARGUMENT, "aligned"),
+    (dict(S=0), _lib.VX_ERR_INVALID_ARGUMENT, ">= 1"),
+    (dict(D=96), _lib.VX_ERR_UNSUPPORTED, "head_dim"),
+    (dict(H=65), _lib.VX_ERR_UNSUPPORTED, "8192"),
+    (dict(per_head=2), _lib.VX_ERR_INVALID_ARGUMENT, "per_head"),
+    (dict(w=A + 4), _lib.VX_ERR_INVALID_ARGUMENT, "weight"),
+    (dict(eps=-1.0), _lib.VX_ERR_INVALID_ARGUMENT, "eps"),
+    (dict(sin=None), _lib.VX_ERR_INVALID_ARGUMENT, "both"),
+    (dict(cos=A + 4), _lib.VX_ERR_INVALID_ARGUMENT, "aligned"),
+    (dict(tab=60), _lib.VX_ERR_INVALID_ARGUMENT, "rope_stride"),
+    (dict(tab=66), _lib.VX_ERR_INVALID_ARGUMENT, "rope_stride"),
+    (dict(xs=(5120, 12)), _lib.VX_ERR_INVALID_ARGUMENT, "multiples of 8"),
+    (dict(out=A, os_=(8192, 1024)), _lib.VX_ERR_INVALID_ARGUMENT, "in-place"),
+])
+def test_prologue_check_rejects(kw, code, frag):
+    assert _prologue_check(**kw) == code
+    assert frag in _lib.last_error()

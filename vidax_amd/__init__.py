@@ -4,11 +4,15 @@ Drop-in replacements for the reference's attention entry points:
   dot_product_attention, local_attention   (src/vidax/core/attention.py)
   masked_self_attention                   (src/vidax/models/hunyuan_video/common/dit_layers.py)
   neighborhood_attention_3d               (src/vidax/models/ltx2_5/diffusion_vae.py)
+and the q/k prologue in front of them:
+  rms_norm, create_rope3d_freqs, apply_rope3d, qk_norm_rope
+                                          (src/vidax/core/attention.py, rope3d.py)
 all backed by libvx_attn.so (C ABI: include/vx_attn.h).
 """
 from .attention import (dot_product_attention, flash_attention, local_attention,
                         masked_self_attention)
 from .natten import neighborhood_attention_3d
+from .prologue import apply_rope3d, create_rope3d_freqs, qk_norm_rope, rms_norm
 
 __all__ = [
     "dot_product_attention",
@@ -16,4 +20,8 @@ __all__ = [
     "local_attention",
     "masked_self_attention",
     "neighborhood_attention_3d",
+    "rms_norm",
+    "create_rope3d_freqs",
+    "apply_rope3d",
+    "qk_norm_rope",
 ]

@@ -27,6 +27,8 @@ EXPORTED_SYMBOLS = (
     "vx_na3d_fwd",
     "vx_na3d_check",
     "vx_debug_inject_error",
+    "vx_rmsnorm_rope_fwd",
+    "vx_rmsnorm_rope_check",
 )
 
 _lock = threading.Lock()
@@ -41,6 +43,7 @@ _i64p = ctypes.POINTER(ctypes.c_int64)
 _FLASH_ARGS = [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32,
                _i64p, _i64p, _i64p, _i64p, _f32]
 _NA3D_ARGS = [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32]
+_PROLOGUE_ARGS = [_p, _p, _p, _f32, _i32, _p, _p, _i64, _i32, _i32, _i32, _i32, _i64p, _i64p]
 
 
 class VxError(RuntimeError):
@@ -77,6 +80,10 @@ def lib() -> ctypes.CDLL:
             h.vx_na3d_fwd.argtypes = _NA3D_ARGS + [_p]
             h.vx_na3d_check.restype = _i32
             h.vx_na3d_check.argtypes = _NA3D_ARGS
+            h.vx_rmsnorm_rope_fwd.restype = _i32
+            h.vx_rmsnorm_rope_fwd.argtypes = _PROLOGUE_ARGS + [_p]
+            h.vx_rmsnorm_rope_check.restype = _i32
+            h.vx_rmsnorm_rope_check.argtypes = _PROLOGUE_ARGS
             h.vx_debug_inject_error.restype = None
             h.vx_debug_inject_error.argtypes = [_i32]
             _lib = h
@@ -97,6 +104,10 @@ def raise_for(code: int) -> None:
     if code == VX_ERR_UNSUPPORTED:
         raise NotImplementedError(f"vidax_amd: {msg}")
     raise VxError(code, msg)
+
+
+def strides2(strides) -> ctypes.Array:
+    return (ctypes.c_int64 * 2)(*[int(s) for s in strides])
 
 
 def strides3(strides) -> ctypes.Array:

@@ -1,0 +1,141 @@
+// Fused attention prologue for gfx950: RMSNorm of q or k (over the whole
+// projected row or per head) followed by the 3D rotary embedding, in one pass
+// over HBM (read the bf16 row once, write the bf16 result once).
+//
+// Per token row x (n_heads * head_dim bf16 values, one wave per row):
+//   norm:  y = bf16( bf16(x * rsqrt(mean(x^2) + eps)) * bf16(w) )
+//          mean over the whole row (group = row) or over each head (group =
+//          head_dim); fp32 statistics. Skipped when no weight is given.
+//   rope:  adjacent pairs (y[2j], y[2j+1]) of every head are rotated by the
+//          token's (cos[j], sin[j]) in fp32 and rounded to bf16. Skipped when
+//          no tables are given.
+// These are the dtype points of the reference's RMSNorm (normalise in fp32,
+// cast, multiply by the cast weight) and apply_rope3d (fp32 rotation, cast).
+//
+// Layout: row s of batch b starts at x + b*x_bstride + s*x_sstride (elements)
+// and is contiguous; lane l of the wave owns the 16-byte chunks l, l + 64, ...
+// of the row, so every load and store is one coalesced 1 KiB wave access.
+#include "vx_gfx950.hpp"
+#include "vx_kernels.h"
+
+namespace vx {
+namespace {
+
+constexpr int kWavesPerBlock = 4;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Sum over aligned groups of n lanes (n = head_dim / 8: the lanes whose
+// chunks make up one head in the same iteration; n divides 64).
+__device__ __forceinline__ float group_sum(float v, int n) {
+  for (int off = n >> 1; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float rsqrt_ieee(float x) { return 1.0f / __builtin_sqrtf(x); }
+
+__device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
+
+template <int NCHUNK>
+__global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const PrologueArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (row >= (int64_t)a.B * a.S) return;  // whole waves only
+  const int b = (int)(row / a.S);
+  const int s = (int)(row - (int64_t)b * a.S);
+  const int row_len = a.H * a.D;
+  const int n_chunks = row_len / 8;
+  const bf16* xr = (const bf16*)a.x + b * a.x_bstride + s * a.x_sstride;
+  bf16* orow = (bf16*)a.out + b * a.o_bstride + s * a.o_sstride;
+
+  bf16x8 v[NCHUNK];
+  float ss[NCHUNK];
+#pragma unroll
+  for (int i = 0; i < NCHUNK; ++i) {
+    const int c = lane + 64 * i;
+    ss[i] = 0.f;
+    if (c < n_chunks) {
+      v[i] = *(const bf16x8*)(xr + c * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss[i] = __builtin_fmaf((float)v[i][e], (float)v[i][e], ss[i]);
+    }
+  }
+
+  if (a.weight != nullptr) {
+    float rinv_row = 0.f;
+    if (!a.per_head) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < NCHUNK; ++i) t += ss[i];
+      rinv_row = rsqrt_ieee(wave_sum(t) / (float)row_len + a.eps);
+    }
+#pragma unroll
+    for (int i = 0; i < NCHUNK; ++i) {
+      const int c = lane + 64 * i;
+      // per head: the head_dim / 8 lanes of an aligned group share a head
+      float rinv = rinv_row;
+      if (a.per_head) rinv = rsqrt_ieee(group_sum(ss[i], a.D / 8) / (float)a.D + a.eps);
+      if (c < n_chunks) {
+        const f32x4 w0 = *(const f32x4*)(a.weight + c * 8);
+        const f32x4 w1 = *(const f32x4*)(a.weight + c * 8 + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float n = (float)to_bf16((float)v[i][e] * rinv);
+          const float w = (float)to_bf16(e < 4 ? w0[e] : w1[e - 4]);
+          v[i][e] = to_bf16(n * w);
+        }
+      }
+    }
+  }
+
+  if (a.cos != nullptr) {
+    const float* cr = a.cos + (int64_t)s * a.tab_stride;
+    const float* sr = a.sin + (int64_t)s * a.tab_stride;
+#pragma unroll
+    for (int i = 0; i < NCHUNK; ++i) {
+      const int c = lane + 64 * i;
+      if (c < n_chunks) {
+        const int j0 = ((c * 8) % a.D) / 2;  // first pair of the chunk within its head
+        const f32x4 cs = *(const f32x4*)(cr + j0);
+        const f32x4 sn = *(const f32x4*)(sr + j0);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const float x1 = (float)v[i][2 * p], x2 = (float)v[i][2 * p + 1];
+          v[i][2 * p] = to_bf16(x1 * cs[p] - x2 * sn[p]);
+          v[i][2 * p + 1] = to_bf16(x2 * cs[p] + x1 * sn[p]);
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < NCHUNK; ++i) {
+    const int c = lane + 64 * i;
+    if (c < n_chunks) *(bf16x8*)(orow + c * 8) = v[i];
+  }
+}
+
+template <int NCHUNK>
+int launch(const PrologueArgs& a, hipStream_t st) {
+  const int64_t rows = (int64_t)a.B * a.S;
+  dim3 grid((unsigned)((rows + kWavesPerBlock - 1) / kWavesPerBlock));
+  hipLaunchKernelGGL((qk_prologue_kernel<NCHUNK>), grid, dim3(kWavesPerBlock * 64), 0, st, a);
+  return (int)hipGetLastError();
+}
+
+}  // namespace
+
+int launch_qk_prologue(const PrologueArgs& a, void* stream) {
+  hipStream_t st = (hipStream_t)stream;
+  const int chunks_per_lane = (a.H * a.D / 8 + 63) / 64;
+  if (chunks_per_lane <= 4) return launch<4>(a, st);
+  if (chunks_per_lane <= 8) return launch<8>(a, st);
+  if (chunks_per_lane <= 16) return launch<16>(a, st);
+  return (int)hipErrorNotSupported;
+}
+
+}  // namespace vx

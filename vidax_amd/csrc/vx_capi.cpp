@@ -2,7 +2,7 @@
 //
 // Plain C++ with no HIP dependency: argument checks, error reporting and the
 // failure-injection hook run on a host without a GPU. The kernels are reached
-// through vx::launch_* (flash_fwd.hip, na3d_fwd.hip).
+// through vx::launch_* (flash_fwd.hip, na3d_fwd.hip, qk_prologue.hip).
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -164,6 +164,64 @@ int32_t na3d_check(const void* q, const void* k, const void* v, const void* out,
   return ok();
 }
 
+int32_t prologue_check(const void* x, const void* out, const float* weight, float eps, int32_t per_head,
+                       const float* rope_cos, const float* rope_sin, int64_t rope_stride, int32_t B, int32_t S,
+                       int32_t H, int32_t D, const int64_t* xs_in, const int64_t* os_in, vx::PrologueArgs* args) {
+  if (x == nullptr || out == nullptr) return fail(VX_ERR_INVALID_ARGUMENT, "x and out must be non-NULL");
+  if (!aligned16(x) || !aligned16(out)) return fail(VX_ERR_INVALID_ARGUMENT, "x and out must be 16-byte aligned");
+  if (B < 1 || S < 1 || H < 1)
+    return fail(VX_ERR_INVALID_ARGUMENT, "batch (%d), seq (%d) and num_heads (%d) must be >= 1", B, S, H);
+  if (D != 64 && D != 128)
+    return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 64 and 128)", D);
+  if ((int64_t)H * D > 8192)
+    return fail(VX_ERR_UNSUPPORTED, "rows of num_heads * head_dim = %lld exceed the supported 8192",
+                (long long)H * D);
+  if (per_head != 0 && per_head != 1) return fail(VX_ERR_INVALID_ARGUMENT, "per_head_norm must be 0 or 1");
+  if (weight != nullptr) {
+    if (!aligned16(weight)) return fail(VX_ERR_INVALID_ARGUMENT, "weight must be 16-byte aligned");
+    if (!(eps >= 0.f) || !std::isfinite(eps))
+      return fail(VX_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0 (got %g)", (double)eps);
+  }
+  if ((rope_cos == nullptr) != (rope_sin == nullptr))
+    return fail(VX_ERR_INVALID_ARGUMENT, "rope_cos and rope_sin must both be given or both be NULL");
+  if (rope_cos != nullptr) {
+    if (!aligned16(rope_cos) || !aligned16(rope_sin))
+      return fail(VX_ERR_INVALID_ARGUMENT, "rope_cos and rope_sin must be 16-byte aligned");
+    if (rope_stride < D / 2 || rope_stride % 4 != 0)
+      return fail(VX_ERR_INVALID_ARGUMENT, "rope_stride (%lld) must be a multiple of 4 and >= head_dim / 2 = %d",
+                  (long long)rope_stride, D / 2);
+  }
+  const int64_t row = (int64_t)H * D;
+  int64_t xs[2] = {S * row, row}, os[2] = {S * row, row};
+  if (xs_in != nullptr) xs[0] = xs_in[0], xs[1] = xs_in[1];
+  if (os_in != nullptr) os[0] = os_in[0], os[1] = os_in[1];
+  for (int i = 0; i < 2; ++i) {
+    if (xs[i] < 0 || xs[i] % 8 != 0 || os[i] < 0 || os[i] % 8 != 0)
+      return fail(VX_ERR_INVALID_ARGUMENT, "strides must be non-negative multiples of 8 elements");
+  }
+  if (x == out && (xs[0] != os[0] || xs[1] != os[1]))
+    return fail(VX_ERR_INVALID_ARGUMENT, "in-place use (out == x) needs identical strides");
+  if (args != nullptr) {
+    args->x = x;
+    args->out = const_cast<void*>(out);
+    args->weight = weight;
+    args->cos = rope_cos;
+    args->sin = rope_sin;
+    args->eps = eps;
+    args->per_head = per_head;
+    args->B = B;
+    args->S = S;
+    args->H = H;
+    args->D = D;
+    args->x_bstride = xs[0];
+    args->x_sstride = xs[1];
+    args->o_bstride = os[0];
+    args->o_sstride = os[1];
+    args->tab_stride = rope_stride;
+  }
+  return ok();
+}
+
 int32_t injected() {
   const int32_t code = g_inject.load(std::memory_order_relaxed);
   if (code != 0) return fail(code, "error injected by vx_debug_inject_error(%d)", code);
@@ -174,7 +232,7 @@ int32_t injected() {
 
 extern "C" {
 
-int32_t vx_abi_version(void) { return 10100; }
+int32_t vx_abi_version(void) { return 10200; }
 
 const char* vx_last_error(void) { return g_error; }
 
@@ -223,6 +281,28 @@ int32_t vx_na3d_fwd(const void* q, const void* k, const void* v, void* out, int3
   if ((rc = injected()) != VX_OK) return rc;
   const int err = vx::launch_na3d_fwd(args, stream);
   if (err != 0) return fail(VX_ERR_LAUNCH, "neighbourhood attention launch failed (hipError_t %d)", err);
+  return ok();
+}
+
+int32_t vx_rmsnorm_rope_check(const void* x, const void* out, const float* weight, float eps, int32_t per_head_norm,
+                              const float* rope_cos, const float* rope_sin, int64_t rope_stride, int32_t batch,
+                              int32_t seq, int32_t num_heads, int32_t head_dim, const int64_t* x_strides,
+                              const int64_t* out_strides) {
+  return prologue_check(x, out, weight, eps, per_head_norm, rope_cos, rope_sin, rope_stride, batch, seq, num_heads,
+                        head_dim, x_strides, out_strides, nullptr);
+}
+
+int32_t vx_rmsnorm_rope_fwd(const void* x, void* out, const float* weight, float eps, int32_t per_head_norm,
+                            const float* rope_cos, const float* rope_sin, int64_t rope_stride, int32_t batch,
+                            int32_t seq, int32_t num_heads, int32_t head_dim, const int64_t* x_strides,
+                            const int64_t* out_strides, void* stream) {
+  vx::PrologueArgs args;
+  int32_t rc = prologue_check(x, out, weight, eps, per_head_norm, rope_cos, rope_sin, rope_stride, batch, seq,
+                              num_heads, head_dim, x_strides, out_strides, &args);
+  if (rc != VX_OK) return rc;
+  if ((rc = injected()) != VX_OK) return rc;
+  const int err = vx::launch_qk_prologue(args, stream);
+  if (err != 0) return fail(VX_ERR_LAUNCH, "rmsnorm/rope launch failed (hipError_t %d)", err);
   return ok();
 }
 

@@ -35,8 +35,21 @@ struct Na3dArgs {
   float scale;
 };
 
-// Both return a hipError_t value (0 on success).
+struct PrologueArgs {
+  const void* x;        // bf16 rows of H * D
+  void* out;            // bf16, same row layout
+  const float* weight;  // H * D (whole-row norm) or H * D (per-head norm, per channel); NULL = no norm
+  const float* cos;     // (S, >= D/2) rows at tab_stride; NULL = no rotation
+  const float* sin;
+  float eps;
+  int32_t per_head;     // 0: mean over the whole row, 1: over each head
+  int32_t B, S, H, D;
+  int64_t x_bstride, x_sstride, o_bstride, o_sstride, tab_stride;  // elements
+};
+
+// All return a hipError_t value (0 on success).
 int launch_flash_fwd(const FlashArgs& a, void* stream);
 int launch_na3d_fwd(const Na3dArgs& a, void* stream);
+int launch_qk_prologue(const PrologueArgs& a, void* stream);
 
 }  // namespace vx
