@@ -40,7 +40,9 @@ __device__ __forceinline__ float rsqrt_ieee(float x) { return 1.0f / __builtin_s
 
 __device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
 
-template <int NCHUNK>
+// NCHUNK: 16-byte chunks per lane (exact); FULL: the row is a whole number of
+// 1 KiB wave accesses, so no lane is ever idle and no chunk needs a bounds test.
+template <int NCHUNK, bool FULL>
 __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const PrologueArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
@@ -49,6 +51,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const 
   const int s = (int)(row - (int64_t)b * a.S);
   const int row_len = a.H * a.D;
   const int n_chunks = row_len / 8;
+  auto live = [&](int c) { return FULL || c < n_chunks; };
   const bf16* xr = (const bf16*)a.x + b * a.x_bstride + s * a.x_sstride;
   bf16* orow = (bf16*)a.out + b * a.o_bstride + s * a.o_sstride;
 
@@ -58,7 +61,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const 
   for (int i = 0; i < NCHUNK; ++i) {
     const int c = lane + 64 * i;
     ss[i] = 0.f;
-    if (c < n_chunks) {
+    if (live(c)) {
       v[i] = *(const bf16x8*)(xr + c * 8);
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss[i] = __builtin_fmaf((float)v[i][e], (float)v[i][e], ss[i]);
@@ -79,7 +82,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const 
       // per head: the head_dim / 8 lanes of an aligned group share a head
       float rinv = rinv_row;
       if (a.per_head) rinv = rsqrt_ieee(group_sum(ss[i], a.D / 8) / (float)a.D + a.eps);
-      if (c < n_chunks) {
+      if (live(c)) {
         const f32x4 w0 = *(const f32x4*)(a.weight + c * 8);
         const f32x4 w1 = *(const f32x4*)(a.weight + c * 8 + 4);
 #pragma unroll
@@ -98,7 +101,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const 
 #pragma unroll
     for (int i = 0; i < NCHUNK; ++i) {
       const int c = lane + 64 * i;
-      if (c < n_chunks) {
+      if (live(c)) {
         const int j0 = ((c * 8) % a.D) / 2;  // first pair of the chunk within its head
         const f32x4 cs = *(const f32x4*)(cr + j0);
         const f32x4 sn = *(const f32x4*)(sr + j0);
@@ -115,7 +118,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const 
 #pragma unroll
   for (int i = 0; i < NCHUNK; ++i) {
     const int c = lane + 64 * i;
-    if (c < n_chunks) *(bf16x8*)(orow + c * 8) = v[i];
+    if (live(c)) *(bf16x8*)(orow + c * 8) = v[i];
   }
 }
 
@@ -123,7 +126,10 @@ template <int NCHUNK>
 int launch(const PrologueArgs& a, hipStream_t st) {
   const int64_t rows = (int64_t)a.B * a.S;
   dim3 grid((unsigned)((rows + kWavesPerBlock - 1) / kWavesPerBlock));
-  hipLaunchKernelGGL((qk_prologue_kernel<NCHUNK>), grid, dim3(kWavesPerBlock * 64), 0, st, a);
+  if ((a.H * a.D) % 512 == 0)
+    hipLaunchKernelGGL((qk_prologue_kernel<NCHUNK, true>), grid, dim3(kWavesPerBlock * 64), 0, st, a);
+  else
+    hipLaunchKernelGGL((qk_prologue_kernel<NCHUNK, false>), grid, dim3(kWavesPerBlock * 64), 0, st, a);
   return (int)hipGetLastError();
 }
 
@@ -131,11 +137,25 @@ int launch(const PrologueArgs& a, hipStream_t st) {
 
 int launch_qk_prologue(const PrologueArgs& a, void* stream) {
   hipStream_t st = (hipStream_t)stream;
-  const int chunks_per_lane = (a.H * a.D / 8 + 63) / 64;
-  if (chunks_per_lane <= 4) return launch<4>(a, st);
-  if (chunks_per_lane <= 8) return launch<8>(a, st);
-  if (chunks_per_lane <= 16) return launch<16>(a, st);
-  return (int)hipErrorNotSupported;
+  switch ((a.H * a.D / 8 + 63) / 64) {  // chunks per lane
+    case 1: return launch<1>(a, st);
+    case 2: return launch<2>(a, st);
+    case 3: return launch<3>(a, st);
+    case 4: return launch<4>(a, st);
+    case 5: return launch<5>(a, st);
+    case 6: return launch<6>(a, st);
+    case 7: return launch<7>(a, st);
+    case 8: return launch<8>(a, st);
+    case 9: return launch<9>(a, st);
+    case 10: return launch<10>(a, st);
+    case 11: return launch<11>(a, st);
+    case 12: return launch<12>(a, st);
+    case 13: return launch<13>(a, st);
+    case 14: return launch<14>(a, st);
+    case 15: return launch<15>(a, st);
+    case 16: return launch<16>(a, st);
+    default: return (int)hipErrorNotSupported;
+  }
 }
 
 }  // namespace vx
