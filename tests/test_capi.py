@@ -90,7 +90,10 @@ def test_na3d_check():
     assert _na_check(W=200, kw=57) == _lib.VX_OK
     assert _na_check(W=200, kw=58) == _lib.VX_ERR_UNSUPPORTED
     assert _na_check(kt=0) == _lib.VX_ERR_INVALID_ARGUMENT
-    assert _na_check(D=64) == _lib.VX_ERR_UNSUPPORTED
+    assert _na_check(D=64) == _lib.VX_OK                             # LTX-2.5 VAE head dim
+    assert _na_check(D=64, W=200, kw=25) == _lib.VX_OK
+    assert _na_check(D=64, W=200, kw=27) == _lib.VX_ERR_UNSUPPORTED
+    assert _na_check(D=96) == _lib.VX_ERR_UNSUPPORTED
     assert _na_check(T=0) == _lib.VX_ERR_INVALID_ARGUMENT
     assert _na_check(k=A + 1) == _lib.VX_ERR_INVALID_ARGUMENT
     assert _na_check(scale=float("nan")) == _lib.VX_ERR_INVALID_ARGUMENT

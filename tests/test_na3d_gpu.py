@@ -62,6 +62,27 @@ def test_na3d_small(gpu, shape, ks, seed):
     _check(out.float().cpu().numpy(), O.na3d(q, k, v, ks), "oracle")
 
 
+NA_D64_CASES = [
+    # LTX-2.5 diffusion-VAE head dim 64 (src/vidax/models/ltx2_5/configs.py:194-203)
+    ((1, 3, 8, 16, 2), (3, 7, 7), 50),
+    ((1, 4, 6, 9, 3), (3, 5, 5), 51),
+    ((2, 5, 13, 21, 1), (3, 5, 5), 52),
+    ((1, 12, 13, 24, 2), (11, 11, 11), 53),   # stage-5 window
+    ((1, 3, 9, 40, 4), (3, 3, 25), 54),       # widest x window for head dim 64
+]
+
+
+@pytest.mark.parametrize("shape,ks,seed", NA_D64_CASES)
+def test_na3d_head_dim_64(gpu, shape, ks, seed):
+    from vidax_amd import neighborhood_attention_3d
+    B, T, H, W, NH = shape
+    _say(f"na3d D=64 shape={shape} kernel={ks} seed={seed}")
+    q, k, v = O.make_na3d_inputs(B, T, H, W, NH, 64, seed)
+    out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), ks)
+    torch.cuda.synchronize()
+    _check(out.float().cpu().numpy(), O.na3d(q, k, v, ks), "oracle")
+
+
 def test_na3d_window_one_is_identity(gpu):
     from vidax_amd import neighborhood_attention_3d
     _say("na3d window (1,1,1) identity")

@@ -252,25 +252,35 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
 // streamed through LDS kRows at a time (2 rows for SEG = 16, 1 for SEG = 32),
 // K and V in separate two-slot rings filled by the DMA path one step ahead;
 // each wave reads the SEG-wide x window it needs from the step's rows, one
-// 32-key chunk. Step s issues QK^T(s+1) and PV(s-1) as one 16-slot block
-// interleaved with the masking and softmax of chunk s (as in the flash
-// kernel), so the matrix cores and the VALU work of a wave overlap. With 80
-// (64) KiB of LDS and at most 256 VGPRs two workgroups share a CU.
+// 32-key chunk. Step s issues QK^T(s+1) and PV(s-1) as one block of
+// D/16 + D/16 MFMA slots interleaved with the masking and softmax of chunk s
+// (as in the flash kernel), so the matrix cores and the VALU work of a wave
+// overlap. With at most 80 KiB of LDS and 256 VGPRs two workgroups share a
+// CU. Head dims 128 and 64 (the LTX-2.5 diffusion VAE's) are instantiated.
 
-template <int SEG>
+template <int SEG, int D>
 struct PipeCfg {
   static constexpr int kWaves = 4;
   static constexpr int kThreads = kWaves * 64;
   static constexpr int kBrickY = 4, kBrickX = 32;
+  static constexpr int kRB = D * 2;                      // bytes of one key row
+  static constexpr int kChunks = kRB / 16;               // 16-byte chunks per key row (16 or 8)
+  static constexpr int kKeysPerCopy = 1024 / kRB;        // key rows per 1 KiB DMA copy (4 or 8)
   static constexpr int kRows = SEG == 16 ? 2 : 1;        // key rows per step
   static constexpr int kNS = SEG == 16 ? 40 : 64;        // key slots per LDS row (>= 24 + SEG)
-  static constexpr int kRowL = kNS * kRowBytes;          // one LDS key row
+  static constexpr int kRowL = kNS * kRB;                // one LDS key row
   static constexpr int kSlot = kRows * kRowL;            // one ring slot: one tensor, one step
   static constexpr int kK = 0, kV = 2 * kSlot;           // K slots 0,1 then V slots 0,1
   static constexpr int kSmem = 4 * kSlot;
-  static constexpr int kCopies = kRows * kNS / 4;        // 1 KiB DMA copies per tensor per step
-  static_assert(kCopies % kWaves == 0, "copies split evenly over the waves");
-  static constexpr int kCopiesPerWave = kCopies / kWaves;
+  static constexpr int kCopies = kRows * kNS / kKeysPerCopy;  // DMA copies per tensor per step
+  // copies past kCopies repeat the last one (same bytes, same place), so every
+  // wave issues the same number of copies
+  static constexpr int kCopiesPerWave = (kCopies + kWaves - 1) / kWaves;
+  static constexpr int kQK = D / 16;                     // MFMAs of QK^T per chunk
+  static constexpr int kPV = 2 * (D / 32);               // MFMAs of PV per chunk
+  static constexpr int kSlots = kQK + kPV;
+  static constexpr int kScoresPerSlot = 16 / kSlots;     // softmax work per slot (1 or 2)
+  static_assert(kNS % kKeysPerCopy == 0, "whole copies per row");
 };
 
 __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_row) {
@@ -291,10 +301,11 @@ __device__ __forceinline__ void wait_vmem() {
 
 __device__ __forceinline__ bool is_nan_bits(float x) { return (__float_as_uint(x) & 0x7fffffffu) > 0x7f800000u; }
 
-template <int SEG>
+template <int SEG, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
-  using C = PipeCfg<SEG>;
+  using C = PipeCfg<SEG, D>;
+  constexpr int kRowBytes = C::kRB;
   __shared__ __attribute__((aligned(16))) unsigned char smem[C::kSmem];
   VX_LDS unsigned char* const lds = (VX_LDS unsigned char*)smem;
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
@@ -354,36 +365,37 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
     xlim[i] = (unsigned)(p - sx) < (unsigned)kw ? __builtin_inff() : -__builtin_inff();
   }
 
-  const int64_t tok_stride = (int64_t)a.NH * kD;
-  const int64_t head_off = (int64_t)b * T * Hs * W * tok_stride + (int64_t)head * kD;
+  const int64_t tok_stride = (int64_t)a.NH * D;
+  const int64_t head_off = (int64_t)b * T * Hs * W * tok_stride + (int64_t)head * D;
   const bf16* qg = (const bf16*)a.q + head_off;
   const bf16* kg = (const bf16*)a.k + head_off;
   const bf16* vg = (const bf16*)a.v + head_off;
   bf16* og = (bf16*)a.o + head_off;
   auto token = [&](int tt, int yy, int xx) -> int64_t { return ((int64_t)tt * Hs + yy) * W + xx; };
 
-  bf16x8 qr[8];
+  bf16x8 qr[C::kQK];
   {
     const bf16* p = qg + token(t, yqc, xqc) * tok_stride + hf * 8;
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
+    for (int ds = 0; ds < C::kQK; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
   }
 
-  // ---- DMA of one step of one tensor: copy i covers LDS row i / (kNS/4) of
-  // the slot and key slots 4*(i % (kNS/4)) + 0..3; wave w issues copies
-  // w, w + 4, ... The lane-dependent part of each copy's source (x position,
-  // swizzled 16-byte chunk) is fixed for the workgroup; the row tokens change
-  // per step and are scalar.
-  const int srow = lane >> 4, scol = lane & 15;
+  // ---- DMA of one step of one tensor: copy i covers LDS row i / (kNS/n) of
+  // the slot and key slots n*(i % (kNS/n)) + 0..n-1 (n = kKeysPerCopy); wave
+  // w issues copies w, w + 4, ... The lane-dependent part of each copy's
+  // source (x position, swizzled 16-byte chunk) is fixed for the workgroup;
+  // the row tokens change per step and are scalar.
+  constexpr int kGroups = C::kNS / C::kKeysPerCopy;  // copies per LDS row
+  const int srow = lane / C::kChunks, scol = lane % C::kChunks;
   int64_t dma_off[C::kCopiesPerWave];
   int dma_dst[C::kCopiesPerWave], dma_row[C::kCopiesPerWave];
 #pragma unroll
   for (int p = 0; p < C::kCopiesPerWave; ++p) {
-    const int i = wave + C::kWaves * p;
-    const int g = i % (C::kNS / 4);
-    const int pos = 4 * g + srow;
-    dma_row[p] = i / (C::kNS / 4);
-    dma_dst[p] = dma_row[p] * C::kRowL + 4 * g * kRowBytes;
+    const int i = min(wave + C::kWaves * p, C::kCopies - 1);
+    const int g = i % kGroups;
+    const int pos = C::kKeysPerCopy * g + srow;
+    dma_row[p] = i / kGroups;
+    dma_dst[p] = dma_row[p] * C::kRowL + C::kKeysPerCopy * g * kRowBytes;
     dma_off[p] = (int64_t)min(X_lo + pos, W - 1) * tok_stride + ((scol ^ row_swizzle(pos)) * 8);
   }
   // Box rows are walked with cursors (row index, its y in the box, its token
@@ -455,10 +467,11 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   auto kfrag = [&](const VX_LDS unsigned char* kb, int ds) -> bf16x8 {
     return *(const VX_LDS bf16x8*)(kb + koff[ds & 3] + (ds >> 2) * 128);
   };
+  constexpr int kDB = D / 32;  // 32-wide d blocks of O
 
-  f32x16 O[4];
+  f32x16 O[kDB];
 #pragma unroll
-  for (int db = 0; db < 4; ++db) O[db] = f32x16{};
+  for (int db = 0; db < kDB; ++db) O[db] = f32x16{};
   float m_run = kNegBig, l_run = 0.f;
   const float c2 = a.scale * kLog2e;
   const bf16x2 one2 = {(bf16)1.0f, (bf16)1.0f};
@@ -469,14 +482,13 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   Cursor vcur = first;  // rows of the next V step to issue (and of the chunk being masked)
   issue(kg, C::kK, kcur);
   issue(kg, C::kK + C::kSlot, kcur);
-#pragma unroll
-  for (int p = 0; p < C::kSlot / (C::kThreads * 16); ++p)
-    *(VX_LDS u32x4*)(lds + C::kV + C::kSlot + (p * C::kThreads + threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
+  for (int off = threadIdx.x * 16; off < C::kSlot; off += C::kThreads * 16)
+    *(VX_LDS u32x4*)(lds + C::kV + C::kSlot + off) = u32x4{0, 0, 0, 0};
   wait_vmem<0>();
   __syncthreads();
   f32x16 S = f32x16{};
 #pragma unroll
-  for (int ds = 0; ds < 8; ++ds) S = mfma32x32x16(kfrag(lds + C::kK, ds), qr[ds], S);
+  for (int ds = 0; ds < C::kQK; ++ds) S = mfma32x32x16(kfrag(lds + C::kK, ds), qr[ds], S);
   bf16x8 Pp[2] = {bf16x8{}, bf16x8{}};
 
   // One step: consumes S (scores of chunk s) and Pp (probabilities of chunk
@@ -505,29 +517,37 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
 
     const VX_LDS unsigned char* kb = lds + C::kK + ((s + 1) & 1) * C::kSlot;  // K of chunk s+1
     const VX_LDS unsigned char* vb = lds + C::kV + ((s + 1) & 1) * C::kSlot;  // V of chunk s-1
-    auto frag = [&](int i) -> bf16x8 { return i < 8 ? vfrag(vb, i >> 2, i & 3) : kfrag(kb, i - 8); };
+    // PV fragment f < kPV: key half j = f / kDB, d block f % kDB; then QK^T.
+    auto frag = [&](int i) -> bf16x8 {
+      return i < C::kPV ? vfrag(vb, i / kDB, i % kDB) : kfrag(kb, i - C::kPV);
+    };
     Sn = f32x16{};
     float l_tile = 0.f;
     const float mneg = -m_run;
-    bf16x8 fr[16];
+    bf16x8 fr[C::kSlots];
     float pf[16];
     bf16x2 pk[8];
     fr[0] = frag(0);
     fr[1] = frag(1);
-    // 16 slots: slot i issues one MFMA (i < 8: PV(s-1), i >= 8: QK^T(s+1)),
-    // the LDS read two slots ahead, and the mask + exp of score i of chunk s.
+    // kSlots slots: slot i issues one MFMA (i < kPV: PV(s-1), else QK^T(s+1)),
+    // the LDS read two slots ahead, and the mask + exp of kScoresPerSlot
+    // scores of chunk s.
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (i + 2 < 16) fr[i + 2] = frag(i + 2);
-      if (i < 8)
-        O[i & 3] = mfma32x32x16(fr[i], Pp[i >> 2], O[i & 3]);
+    for (int i = 0; i < C::kSlots; ++i) {
+      if (i + 2 < C::kSlots) fr[i + 2] = frag(i + 2);
+      if (i < C::kPV)
+        O[i % kDB] = mfma32x32x16(fr[i], Pp[i / kDB], O[i % kDB]);
       else
-        Sn = mfma32x32x16(fr[i], qr[i - 8], Sn);
-      S[i] = __builtin_fminf(__builtin_fminf(S[i], xlim[i]), rlim[i >> 3]);
-      pf[i] = fast_exp2(__builtin_fmaf(S[i], c2, mneg));
-      if (i & 1) {
-        pk[i >> 1] = bf16x2{(bf16)pf[i - 1], (bf16)pf[i]};
-        l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[i >> 1], one2, l_tile, false);
+        Sn = mfma32x32x16(fr[i], qr[i - C::kPV], Sn);
+#pragma unroll
+      for (int u = 0; u < C::kScoresPerSlot; ++u) {
+        const int e = i * C::kScoresPerSlot + u;
+        S[e] = __builtin_fminf(__builtin_fminf(S[e], xlim[e]), rlim[e >> 3]);
+        pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, mneg));
+        if (e & 1) {
+          pk[e >> 1] = bf16x2{(bf16)pf[e - 1], (bf16)pf[e]};
+          l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[e >> 1], one2, l_tile, false);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -549,7 +569,7 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
       m_run = mn;
       l_run *= alpha;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) O[db] *= alpha;
+      for (int db = 0; db < kDB; ++db) O[db] *= alpha;
       l_tile = 0.f;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -581,7 +601,7 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   {
     const VX_LDS unsigned char* vb = lds + C::kV + ((n_steps - 1) & 1) * C::kSlot;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) O[i & 3] = mfma32x32x16(vfrag(vb, i >> 2, i & 3), Pp[i >> 2], O[i & 3]);
+    for (int i = 0; i < C::kPV; ++i) O[i % kDB] = mfma32x32x16(vfrag(vb, i / kDB, i % kDB), Pp[i / kDB], O[i % kDB]);
   }
 
   const float lt = halves_sum(l_run);
@@ -589,7 +609,7 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   if (q_in) {
     bf16* orow = og + token(t, yq, xq) * tok_stride;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < kDB; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         bf16x4 ov;
@@ -603,18 +623,26 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
 }  // namespace
 
 int launch_na3d_fwd(const Na3dArgs& a, void* stream) {
-  if (a.D != kD) return (int)hipErrorNotSupported;
+  if (a.D != 128 && a.D != 64) return (int)hipErrorNotSupported;
   hipStream_t st = (hipStream_t)stream;
   if (a.kw <= 25) {
     const int n_yb = (a.Hs + 3) / 4;
     const int n_xb = (a.W + 31) / 32;
     dim3 grid((unsigned)a.T * n_yb * n_xb, a.NH, a.B);
-    if (a.kw <= 9)
-      hipLaunchKernelGGL((na3d_pipe_kernel<16>), grid, dim3(256), 0, st, a, n_yb, n_xb);
-    else
-      hipLaunchKernelGGL((na3d_pipe_kernel<32>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+    if (a.D == 128) {
+      if (a.kw <= 9)
+        hipLaunchKernelGGL((na3d_pipe_kernel<16, 128>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+      else
+        hipLaunchKernelGGL((na3d_pipe_kernel<32, 128>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+    } else {
+      if (a.kw <= 9)
+        hipLaunchKernelGGL((na3d_pipe_kernel<16, 64>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+      else
+        hipLaunchKernelGGL((na3d_pipe_kernel<32, 64>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+    }
     return (int)hipGetLastError();
   }
+  if (a.D != kD) return (int)hipErrorNotSupported;  // the per-wave kernel is D = 128 only
   const int n_yb = (a.Hs + kBrickY - 1) / kBrickY;
   const int n_xb = (a.W + kBrickX - 1) / kBrickX;
   const int n_xg = (n_xb + kWaves - 1) / kWaves;

@@ -133,11 +133,15 @@ int32_t na3d_check(const void* q, const void* k, const void* v, const void* out,
                 W, NH);
   if (kt < 1 || kh < 1 || kw < 1)
     return fail(VX_ERR_INVALID_ARGUMENT, "kernel sizes must be >= 1 (got %d, %d, %d)", kt, kh, kw);
-  if (D != 128) return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 128)", D);
+  if (D != 128 && D != 64)
+    return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 64 and 128)", D);
   if (B > 65535 || NH > 65535)
     return fail(VX_ERR_INVALID_ARGUMENT, "batch (%d) and num_heads (%d) must be <= 65535", B, NH);
   if ((kw < W ? kw : W) > 57)
     return fail(VX_ERR_UNSUPPORTED, "kernel_w (clamped to w) = %d exceeds the supported 57", kw < W ? kw : W);
+  if (D == 64 && (kw < W ? kw : W) > 25)
+    return fail(VX_ERR_UNSUPPORTED, "head_dim 64 supports kernel_w (clamped to w) up to 25, got %d",
+                kw < W ? kw : W);
   if (!(scale > 0.f) || !std::isfinite(scale))
     return fail(VX_ERR_INVALID_ARGUMENT, "scale must be positive and finite (got %g)", (double)scale);
   const int64_t tokens = (int64_t)T * Hs * W;
