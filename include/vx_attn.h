@@ -78,6 +78,39 @@ int32_t vx_flash_attn_fwd(const void* q, const void* k, const void* v, void* out
                           void* stream);
 
 /*
+ * vx_flash_attn_fwd plus an additive fp32 bias that depends on the head and
+ * the query as well as the key (T5's relative-position bias, causal or other
+ * boolean masks turned into 0 / -inf):
+ *   logit[b, h, i, j] = scale * q.k + bias[b*bs[0] + h*bs[1] + i*bs[2] + j]
+ *                       (+ the key-only masks, which may be given as well)
+ * bias_strides {batch, head, query} in elements, non-negative multiples of 4
+ * (0 broadcasts, e.g. T5's (1, H, L, L) bias over the batch); keys are
+ * contiguous and every query row must be readable for round_up(seq_k, 64)
+ * elements; bias 16-byte aligned. The bias is read per query row from global
+ * memory, which suits the short sequences that use it (text encoders).
+ *
+ * Replaces the reference's non-kernel branch of dot_product_attention for a
+ * head- or query-dependent bias or boolean mask:
+ *   - src/vidax/core/attention.py:519-533 (jax.nn.dot_product_attention fallback)
+ *   - src/vidax/models/wan/common/t5.py:40-68 (relative-position bias, scale 1)
+ *   - src/vidax/models/cosmos3/dit_layers.py:114-116 (causal text pathway)
+ */
+int32_t vx_flash_attn_bias_fwd(const void* q, const void* k, const void* v, void* out, const int32_t* kv_len,
+                               const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride,
+                               const float* bias, const int64_t* bias_strides, int32_t batch, int32_t seq_q,
+                               int32_t seq_k, int32_t num_heads, int32_t head_dim, const int64_t* q_strides,
+                               const int64_t* k_strides, const int64_t* v_strides, const int64_t* out_strides,
+                               float scale, void* stream);
+
+/* Host-only argument check for vx_flash_attn_bias_fwd (no GPU needed). */
+int32_t vx_flash_attn_bias_check(const void* q, const void* k, const void* v, const void* out, const int32_t* kv_len,
+                                 const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride,
+                                 const float* bias, const int64_t* bias_strides, int32_t batch, int32_t seq_q,
+                                 int32_t seq_k, int32_t num_heads, int32_t head_dim, const int64_t* q_strides,
+                                 const int64_t* k_strides, const int64_t* v_strides, const int64_t* out_strides,
+                                 float scale);
+
+/*
  * Host-only argument check for vx_flash_attn_fwd (no GPU needed): returns what
  * vx_flash_attn_fwd would return for these arguments before launching.
  * Pointers are checked for NULL-ness and alignment only.

@@ -124,14 +124,17 @@ def _softmax_rows(logits: np.ndarray) -> np.ndarray:
 
 
 def attention(q, k, v, scale=None, kv_len=None, key_valid=None, key_bias=None,
-              acc=np.float64, weights_dtype_round=False, q_block=2048):
+              acc=np.float64, weights_dtype_round=False, q_block=2048, bias=None):
     """softmax(scale * q k^T + key_mask) v for (B, Sq, H, D) / (B, Sk, H, D).
 
     Key masks are key-only: `kv_len` (B,) prefix lengths, `key_valid` (B, Sk)
     booleans, `key_bias` (B, Sk) additive logits (may hold -inf). Computed in
     `acc` precision; `weights_dtype_round=True` rounds the softmax weights to
     bf16 before the PV product, as the Hunyuan dense restatement does
-    (`hunyuan_video/common/dit_layers.py:336`).
+    (`hunyuan_video/common/dit_layers.py:336`). `bias`, broadcastable to
+    (B, H, Sq, Sk), is added to the scaled logits as the reference's
+    non-kernel path does with a bias or a 0 / -inf boolean mask
+    (`src/vidax/core/attention.py:533`, `wan/common/t5.py:40-68`).
     """
     q = np.asarray(q)
     k = np.asarray(k)
@@ -141,6 +144,9 @@ def attention(q, k, v, scale=None, kv_len=None, key_valid=None, key_bias=None,
     if scale is None:
         scale = D ** -0.5
     out = np.zeros((B, Sq, H, D), dtype=acc)
+    full = None
+    if bias is not None:
+        full = np.broadcast_to(np.asarray(bias, dtype=np.float64), (B, H, Sq, Sk))
     for b in range(B):
         add = _key_allowed(b, Sk, kv_len, key_valid, key_bias).astype(acc)
         for h in range(H):
@@ -149,6 +155,8 @@ def attention(q, k, v, scale=None, kv_len=None, key_valid=None, key_bias=None,
             for s0 in range(0, Sq, q_block):
                 qq = q[b, s0:s0 + q_block, h, :].astype(acc)
                 logits = (qq @ kk.T) * acc(scale) + add[None, :]
+                if full is not None:
+                    logits = logits + full[b, h, s0:s0 + q_block].astype(acc)
                 w = _softmax_rows(logits)
                 if weights_dtype_round:
                     w = bf16_round(w.astype(np.float32)).astype(acc)

@@ -32,7 +32,7 @@ def test_header_symbols_are_exported():
 
 
 def test_abi_version():
-    assert _lib.lib().vx_abi_version() == 10200
+    assert _lib.lib().vx_abi_version() == 10300
 
 
 def _flash_check(**kw):
@@ -198,3 +198,25 @@ def test_prologue_check_accepts_valid_arguments():
 def test_prologue_check_rejects(kw, code, frag):
     assert _prologue_check(**kw) == code
     assert frag in _lib.last_error()
+
+
+def _bias_check(bias=A, strides=(0, 256 * 256, 256), **kw):
+    args = dict(q=A, k=A, v=A, out=A, kv_len=None, key_valid=None, key_bias=None, stride=0,
+                B=1, Sq=100, Sk=200, H=4, D=128, scale=1.0)
+    args.update(kw)
+    return _lib.lib().vx_flash_attn_bias_check(
+        args["q"], args["k"], args["v"], args["out"], args["kv_len"], args["key_valid"], args["key_bias"],
+        args["stride"], bias, None if strides is None else _lib.strides3(strides), args["B"], args["Sq"],
+        args["Sk"], args["H"], args["D"], None, None, None, None, ctypes.c_float(args["scale"]))
+
+
+def test_flash_bias_check():
+    assert _bias_check() == _lib.VX_OK
+    assert _bias_check(strides=(0, 0, 0)) == _lib.VX_OK                  # fully broadcast
+    assert _bias_check(bias=None) == _lib.VX_ERR_INVALID_ARGUMENT
+    assert _bias_check(bias=A + 4) == _lib.VX_ERR_INVALID_ARGUMENT
+    assert "aligned" in _lib.last_error()
+    assert _bias_check(strides=(0, 256, 258)) == _lib.VX_ERR_INVALID_ARGUMENT
+    assert "multiple of 4" in _lib.last_error()
+    assert _bias_check(strides=None) == _lib.VX_ERR_INVALID_ARGUMENT
+    assert _bias_check(D=64) == _lib.VX_ERR_UNSUPPORTED

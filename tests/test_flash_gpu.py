@@ -240,3 +240,49 @@ def test_flash_config5_zero_query_is_valid_mean(gpu):
     # all weights are exactly 1 in bf16; only fp32 accumulation and the bf16
     # rounding of a ~3e-3-sized output remain
     assert err.max().item() <= 1e-4
+
+
+# ---------------------------------------------------- head/query-dependent bias
+BIAS_CASES = [
+    # B, Sq, Sk, H, seed, bias shape kind
+    (2, 200, 200, 4, 60, "t5"),          # (1, H, L, L) relative-position-style bias, scale 1
+    (1, 130, 130, 2, 61, "causal"),      # boolean (L, L) lower-triangular mask
+    (2, 70, 300, 3, 62, "head_keys"),    # (1, H, 1, Sk): per-head key bias (query-broadcast)
+    (2, 96, 515, 2, 63, "t5_padded"),    # (B, H, Sq, Sk) bias + key padding mask
+]
+
+
+@pytest.mark.parametrize("B,Sq,Sk,H,seed,kind", BIAS_CASES)
+def test_flash_full_bias_and_masks(gpu, B, Sq, Sk, H, seed, kind):
+    """dot_product_attention with a bias or mask that depends on head and/or
+    query -- the reference's jax.nn fallback (attention.py:519-533; T5's
+    relative bias, t5.py:40-68; causal text attention, cosmos3
+    dit_layers.py:114-116) -- against the oracle."""
+    from vidax_amd import dot_product_attention
+    _say(f"flash bias kind={kind} B={B} Sq={Sq} Sk={Sk} H={H} seed={seed}")
+    q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, 128, seed)
+    rng = np.random.default_rng(seed + 1)
+    tq, tk, tv = _t(q, gpu), _t(k, gpu), _t(v, gpu)
+    if kind == "t5":
+        bias = (2.0 * rng.standard_normal((1, H, Sq, Sk))).astype(np.float32)
+        out = dot_product_attention(tq, tk, tv, bias=torch.from_numpy(bias).to(gpu), scale=1.0)
+        ref = O.attention(q, k, v, scale=1.0, bias=bias)
+    elif kind == "causal":
+        causal = np.tril(np.ones((Sq, Sk), bool))
+        out = dot_product_attention(tq, tk, tv, mask=torch.from_numpy(causal).to(gpu))
+        ref = O.attention(q, k, v, bias=np.where(causal, 0.0, -np.inf))
+    elif kind == "head_keys":
+        bias = rng.standard_normal((1, H, 1, Sk)).astype(np.float32)
+        bias[:, 1, :, 40:90] = -np.inf
+        out = dot_product_attention(tq, tk, tv, bias=torch.from_numpy(bias).to(gpu))
+        ref = O.attention(q, k, v, bias=bias)
+    else:
+        bias = rng.standard_normal((B, H, Sq, Sk)).astype(np.float32)
+        valid = np.ones((B, 1, 1, Sk), bool)
+        valid[0, ..., 400:] = False
+        valid[1, ..., 200:260] = False
+        out = dot_product_attention(tq, tk, tv, bias=torch.from_numpy(bias).to(gpu),
+                                    mask=torch.from_numpy(valid).to(gpu))
+        ref = O.attention(q, k, v, bias=bias + np.where(valid, 0.0, -np.inf))
+    torch.cuda.synchronize()
+    _check(out, ref, kind)

@@ -15,7 +15,7 @@ import torch
 from oracle import attention_oracle as O
 
 
-def _sdpa(q, k, v, scale, valid=None, bias=None):
+def _sdpa(q, k, v, scale, valid=None, bias=None, attn_mask=None):
     """torch SDPA in float64 on (B, S, H, D) numpy inputs."""
     tq = torch.from_numpy(np.asarray(q, np.float64)).permute(0, 2, 1, 3)
     tk = torch.from_numpy(np.asarray(k, np.float64)).permute(0, 2, 1, 3)
@@ -25,6 +25,8 @@ def _sdpa(q, k, v, scale, valid=None, bias=None):
         mask = torch.from_numpy(valid)[:, None, None, :]
     if bias is not None:
         mask = torch.from_numpy(np.asarray(bias, np.float64))[:, None, None, :]
+    if attn_mask is not None:
+        mask = attn_mask
     out = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, attn_mask=mask, scale=scale)
     return out.permute(0, 2, 1, 3).numpy()
 
@@ -98,6 +100,19 @@ def test_attention_masks_match_torch_sdpa():
     prefix = np.arange(Sk)[None, :] < kv_len[:, None]
     np.testing.assert_allclose(O.attention(q, k, v, kv_len=kv_len), _sdpa(q, k, v, D ** -0.5, valid=prefix),
                                rtol=1e-10, atol=1e-12)
+
+
+def test_attention_full_bias_matches_torch_sdpa():
+    """Head- and query-dependent additive bias (T5-style) and a causal boolean
+    mask against torch's SDPA with the same (B, H, Sq, Sk) mask."""
+    rng = np.random.default_rng(21)
+    B, Sq, Sk, H, D = 2, 9, 9, 3, 16
+    q, k, v = (rng.standard_normal((B, S, H, D)) for S in (Sq, Sk, Sk))
+    bias = rng.standard_normal((1, H, Sq, Sk)) * 2
+    causal = np.tril(np.ones((Sq, Sk), bool))
+    full = bias + np.where(causal, 0.0, -np.inf)[None, None]
+    ref = _sdpa(q, k, v, 1.0, attn_mask=torch.from_numpy(np.broadcast_to(full, (B, H, Sq, Sk)).copy()))
+    np.testing.assert_allclose(O.attention(q, k, v, scale=1.0, bias=full), ref, atol=1e-10)
 
 
 def test_attention_invariants():

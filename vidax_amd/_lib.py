@@ -29,6 +29,8 @@ EXPORTED_SYMBOLS = (
     "vx_debug_inject_error",
     "vx_rmsnorm_rope_fwd",
     "vx_rmsnorm_rope_check",
+    "vx_flash_attn_bias_fwd",
+    "vx_flash_attn_bias_check",
 )
 
 _lock = threading.Lock()
@@ -43,6 +45,8 @@ _i64p = ctypes.POINTER(ctypes.c_int64)
 _FLASH_ARGS = [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32,
                _i64p, _i64p, _i64p, _i64p, _f32]
 _NA3D_ARGS = [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32]
+_FLASH_BIAS_ARGS = [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64p, _i32, _i32, _i32, _i32, _i32,
+                    _i64p, _i64p, _i64p, _i64p, _f32]
 _PROLOGUE_ARGS = [_p, _p, _p, _f32, _i32, _p, _p, _i64, _i32, _i32, _i32, _i32, _i64p, _i64p]
 
 
@@ -80,6 +84,10 @@ def lib() -> ctypes.CDLL:
             h.vx_na3d_fwd.argtypes = _NA3D_ARGS + [_p]
             h.vx_na3d_check.restype = _i32
             h.vx_na3d_check.argtypes = _NA3D_ARGS
+            h.vx_flash_attn_bias_fwd.restype = _i32
+            h.vx_flash_attn_bias_fwd.argtypes = _FLASH_BIAS_ARGS + [_p]
+            h.vx_flash_attn_bias_check.restype = _i32
+            h.vx_flash_attn_bias_check.argtypes = _FLASH_BIAS_ARGS
             h.vx_rmsnorm_rope_fwd.restype = _i32
             h.vx_rmsnorm_rope_fwd.argtypes = _PROLOGUE_ARGS + [_p]
             h.vx_rmsnorm_rope_check.restype = _i32

@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import ctypes
 import math
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 
@@ -70,13 +70,38 @@ def _last_valid_plus_one(valid: torch.Tensor) -> torch.Tensor:
     return (valid.to(torch.int32) * pos).amax(dim=-1).to(torch.int32).contiguous()
 
 
+def _full_bias(bias, B: int, H: int, Sq: int, Sk: int, dev) -> Tuple[torch.Tensor, Tuple[int, int, int]]:
+    """A (B|1, H|1, Sq|1, Sk) additive bias as the kernel reads it: fp32, keys
+    contiguous, every query row readable for round_up(Sk, 64) keys, 16-byte
+    aligned, strides multiples of 4 (0 for broadcast dims). Copies only when
+    the given tensor does not already have that form."""
+    x = torch.as_tensor(bias, device=dev)
+    while x.dim() < 4:
+        x = x.unsqueeze(0)
+    if x.dim() != 4 or x.shape[-1] != Sk or any(x.shape[i] not in (1, n) for i, n in enumerate((B, H, Sq))):
+        raise ValueError(f"bias of shape {tuple(bias.shape)} is not broadcastable to (B, H, Sq, Sk) = "
+                         f"({B}, {H}, {Sq}, {Sk})")
+    x = x.to(torch.float32)
+    width = (Sk + 63) // 64 * 64
+    ok = (x.stride(3) == 1 and Sk == width and x.data_ptr() % 16 == 0 and
+          all(x.stride(i) % 4 == 0 for i in range(3)))
+    if not ok:
+        pad = torch.zeros(x.shape[:3] + (width,), dtype=torch.float32, device=dev)
+        pad[..., :Sk] = x
+        x = pad
+    strides = tuple(0 if x.shape[i] == 1 else x.stride(i) for i in range(3))
+    return x, strides
+
+
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                     scale: Optional[float] = None,
                     kv_len: Optional[torch.Tensor] = None,
                     key_valid: Optional[torch.Tensor] = None,
                     key_bias: Optional[torch.Tensor] = None,
+                    bias: Optional[torch.Tensor] = None,
                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Non-causal flash attention with optional key-only masks.
+    """Non-causal flash attention with optional key-only masks and an
+    optional additive bias that may also depend on head and query.
 
     q (B, Sq, H, D), k/v (B, Sk, H, D), bf16 on the GPU; returns (B, Sq, H, D).
     scale defaults to 1/sqrt(D) (`src/vidax/core/attention.py:335,524`).
@@ -84,6 +109,10 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     (B, Sk) bool/int: general key validity. key_bias (B, Sk) float: additive
     logits (-inf masks). All masks broadcast over heads and query rows, as
     the reference's segment ids do (`hunyuan_video/common/dit_layers.py:183-186`).
+    bias: fp32-convertible, broadcastable to (B, H, Sq, Sk), added to the
+    scaled logits (T5's relative-position bias, `wan/common/t5.py:40-68`;
+    0 / -inf from a boolean mask). It is read per query row from memory, so
+    it suits the short sequences that use it.
     """
     _check_qkv(q, k, v)
     B, Sq, H, D = q.shape
@@ -111,6 +140,20 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         stride = key_bias_t.shape[1]
     L = _lib.lib()
     stream = torch.cuda.current_stream(dev).cuda_stream
+    if bias is not None:
+        fb, fbs = _full_bias(bias, B, H, Sq, Sk, dev)
+        with torch.cuda.device(dev):
+            rc = L.vx_flash_attn_bias_fwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                kv_len_t.data_ptr() if kv_len_t is not None else None,
+                key_valid_t.data_ptr() if key_valid_t is not None else None,
+                key_bias_t.data_ptr() if key_bias_t is not None else None,
+                stride, fb.data_ptr(), _lib.strides3(fbs), B, Sq, Sk, H, D,
+                _lib.strides3(q.stride()[:3]), _lib.strides3(k.stride()[:3]),
+                _lib.strides3(v.stride()[:3]), _lib.strides3(out.stride()[:3]),
+                ctypes.c_float(scale), ctypes.c_void_p(stream))
+        _lib.raise_for(rc)
+        return out
     with torch.cuda.device(dev):
         rc = L.vx_flash_attn_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
@@ -169,39 +212,39 @@ def dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
     `bias` and `mask` are broadcastable to (B, H, Sq, Sk), as in the
     reference. Key-only forms -- shape (B or 1, 1, 1, Sk), e.g. Cosmos3's
-    (B, 1, 1, Sk) -inf padding bias -- run in the flash kernel (the masked
-    key loop is bounded by the last valid key). Head- or query-dependent
-    biases and masks (T5 relative bias, causal masks) take the reference's
-    materialising fallback there; that path is not part of this build and
-    raises NotImplementedError.
+    (B, 1, 1, Sk) -inf padding bias -- run in the flash kernel's key-mask
+    path (the key loop is bounded by the last valid key). Head- or
+    query-dependent ones -- T5's relative-position bias, causal masks, the
+    reference's `jax.nn.dot_product_attention` fallback -- run in the same
+    kernel with a per-(query, key) bias (a boolean mask becomes 0 / -inf).
     """
     _check_qkv(q, k, v)
     _single_device(mesh)
-    B, _, _, D = q.shape
+    B, Sq, H, D = q.shape
     Sk = k.shape[1]
     sm_scale = D ** -0.5 if scale is None else scale
-    key_bias = key_valid = kv_len = None
+    key_bias = key_valid = kv_len = full = None
     valid = None
     if bias is not None:
         kb = _key_only(torch.as_tensor(bias, device=q.device), B, Sk, "bias")
         if kb is None:
-            raise NotImplementedError(
-                "head- or query-dependent attention bias is not supported by the "
-                "flash kernel (the reference materialises it in XLA)")
-        key_bias = kb.to(torch.float32)
-        valid = key_bias > float("-inf")
+            full = torch.as_tensor(bias, device=q.device).to(torch.float32)
+        else:
+            key_bias = kb.to(torch.float32)
+            valid = key_bias > float("-inf")
     if mask is not None:
         km = _key_only(torch.as_tensor(mask, device=q.device), B, Sk, "mask")
         if km is None:
-            raise NotImplementedError(
-                "head- or query-dependent boolean masks are not supported by the "
-                "flash kernel (the reference materialises them in XLA)")
-        key_valid = km.to(torch.bool)
-        valid = key_valid if valid is None else (valid & key_valid)
+            m = torch.as_tensor(mask, device=q.device).to(torch.bool)
+            add = torch.zeros(m.shape, dtype=torch.float32, device=q.device).masked_fill_(~m, float("-inf"))
+            full = add if full is None else full + add
+        else:
+            key_valid = km.to(torch.bool)
+            valid = key_valid if valid is None else (valid & key_valid)
     if valid is not None:
         kv_len = _last_valid_plus_one(valid)
     return flash_attention(q, k, v, scale=sm_scale, kv_len=kv_len, key_valid=key_valid,
-                           key_bias=key_bias)
+                           key_bias=key_bias, bias=full)
 
 
 def masked_self_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

@@ -49,8 +49,10 @@ constexpr int kSmemBytes = 6 * kTileBytes;    // 96 KiB
 constexpr int kMaskBuf = 6 * kTileBytes;
 constexpr int kMaskSlot = 320;
 constexpr int kMaskRing = 4;
-// Mask kinds (template argument): no mask, validity bytes, additive biases, both.
-constexpr int kMaskNone = 0, kMaskValid = 1, kMaskBias = 2;
+// Mask kinds (template argument, bits): validity bytes per key, additive bias
+// per key, additive bias per (query, key) of each head (read per query row
+// straight from global memory: meant for the short sequences that use it).
+constexpr int kMaskNone = 0, kMaskValid = 1, kMaskBias = 2, kMaskFull = 4;
 constexpr int kLoadsPerWave = (kBN / 4) / kWaves;  // 1 KiB wave loads per tile
 constexpr float kRescaleSlack = 8.0f;         // log2 units
 constexpr float kSumLimit = 256.0f;           // 2^kRescaleSlack
@@ -92,6 +94,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 void flash_fwd_kernel(const FlashArgs a) {
   constexpr bool MASKED = MASK != kMaskNone;
   constexpr int kMaskCopies = (MASK & kMaskValid ? 1 : 0) + (MASK & kMaskBias ? 1 : 0);
+  constexpr bool kFull = (MASK & kMaskFull) != 0;
   __shared__ __attribute__((aligned(16))) unsigned char smem[kSmemBytes + (MASKED ? kMaskRing * kMaskSlot : 0)];
   lds_u8* const lds = (lds_u8*)smem;
 
@@ -228,6 +231,10 @@ void flash_fwd_kernel(const FlashArgs a) {
   float m_run = kNegBig, l_run = 0.f;
 
   const uint8_t* vrow = (MASK & kMaskValid) ? a.key_valid + (int64_t)b * a.key_mask_stride : nullptr;
+  // this lane's query row of the full bias (row of a clamped query past Sq)
+  const float* frow = kFull ? a.full_bias + b * a.fbs[0] + head * a.fbs[1] +
+                                  (int64_t)min(qw0 + col, a.Sq - 1) * a.fbs[2]
+                            : nullptr;
   const float* brow = (MASK & kMaskBias) ? a.key_bias + (int64_t)b * a.key_mask_stride : nullptr;
   // Wave 0 stages tile j's mask (64 validity bytes: lanes 0-3; 64 biases:
   // lanes 0-15) into mask slot j % 4. Mask rows hold whole 64-key tiles.
@@ -315,7 +322,7 @@ void flash_fwd_kernel(const FlashArgs a) {
           }
         slow = slow || __builtin_amdgcn_ballot_w64(hole) != 0;
       }
-      if (MASK & kMaskBias) slow = true;
+      if (MASK & (kMaskBias | kMaskFull)) slow = true;
       stage(kg, klane, a.ks[1], min(t + 3, n_tiles - 1), kKBuf + kb_next * kTileBytes);
       stage_mask(min(t + 3, n_tiles - 1));
       stage(vg, vlane, a.vs[1], min(t + 1, n_tiles - 1), kVBuf + vb_next * kTileBytes);
@@ -329,6 +336,7 @@ void flash_fwd_kernel(const FlashArgs a) {
             const int kbase = key0 + kb * 32 + g * 8 + hf * 4;
             f32x4 bias = {0.f, 0.f, 0.f, 0.f};
             if (MASK & kMaskBias) bias = *(const VX_LDS f32x4*)(mslot + 64 + (kbase - key0) * 4) * kLog2e;
+            if (kFull) bias += *(const f32x4*)(frow + kbase) * kLog2e;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               bool ok = kbase + e < kv_end;
@@ -468,6 +476,14 @@ int launch(const FlashArgs& a, hipStream_t stream) {
 int launch_flash_fwd(const FlashArgs& a, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   const int mask = (a.key_valid != nullptr ? kMaskValid : 0) | (a.key_bias != nullptr ? kMaskBias : 0);
+  if (a.full_bias != nullptr) {
+    switch (mask) {
+      case kMaskValid: return launch<kMaskFull | kMaskValid>(a, s);
+      case kMaskBias: return launch<kMaskFull | kMaskBias>(a, s);
+      case kMaskValid | kMaskBias: return launch<kMaskFull | kMaskValid | kMaskBias>(a, s);
+      default: return launch<kMaskFull>(a, s);
+    }
+  }
   switch (mask) {
     case kMaskValid: return launch<kMaskValid>(a, s);
     case kMaskBias: return launch<kMaskBias>(a, s);

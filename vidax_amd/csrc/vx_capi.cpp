@@ -61,7 +61,8 @@ int32_t flash_check(const void* q, const void* k, const void* v, const void* out
                     const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride, int32_t B,
                     int32_t Sq, int32_t Sk,
                     int32_t H, int32_t D, const int64_t* qs_in, const int64_t* ks_in, const int64_t* vs_in,
-                    const int64_t* os_in, float scale, vx::FlashArgs* args) {
+                    const int64_t* os_in, float scale, vx::FlashArgs* args,
+                    const float* full_bias = nullptr, const int64_t* fb_strides = nullptr) {
   (void)kv_len;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr)
     return fail(VX_ERR_INVALID_ARGUMENT, "q, k, v and out must be non-NULL");
@@ -85,6 +86,14 @@ int32_t flash_check(const void* q, const void* k, const void* v, const void* out
       return fail(VX_ERR_INVALID_ARGUMENT, "key_valid must be 4-byte aligned");
     if (key_bias != nullptr && !aligned16(key_bias))
       return fail(VX_ERR_INVALID_ARGUMENT, "key_bias must be 16-byte aligned");
+  }
+  if (full_bias != nullptr) {
+    if (!aligned16(full_bias)) return fail(VX_ERR_INVALID_ARGUMENT, "bias must be 16-byte aligned");
+    if (fb_strides == nullptr) return fail(VX_ERR_INVALID_ARGUMENT, "bias_strides must be given with bias");
+    for (int i = 0; i < 3; ++i)
+      if (fb_strides[i] < 0 || fb_strides[i] % 4 != 0)
+        return fail(VX_ERR_INVALID_ARGUMENT, "bias_strides[%d] = %lld must be a non-negative multiple of 4", i,
+                    (long long)fb_strides[i]);
   }
   int64_t qs[3], ks[3], vs[3], os[3];
   strides_or_default(qs_in, Sq, H, D, qs);
@@ -117,6 +126,8 @@ int32_t flash_check(const void* q, const void* k, const void* v, const void* out
       args->os[i] = os[i];
     }
     args->scale = scale;
+    args->full_bias = full_bias;
+    for (int i = 0; i < 3; ++i) args->fbs[i] = full_bias != nullptr ? fb_strides[i] : 0;
   }
   return ok();
 }
@@ -236,7 +247,7 @@ int32_t injected() {
 
 extern "C" {
 
-int32_t vx_abi_version(void) { return 10200; }
+int32_t vx_abi_version(void) { return 10300; }
 
 const char* vx_last_error(void) { return g_error; }
 
@@ -262,6 +273,35 @@ int32_t vx_flash_attn_fwd(const void* q, const void* k, const void* v, void* out
   vx::FlashArgs args;
   int32_t rc = flash_check(q, k, v, out, kv_len, key_valid, key_bias, key_mask_stride, batch, seq_q, seq_k,
                            num_heads, head_dim, q_strides, k_strides, v_strides, out_strides, scale, &args);
+  if (rc != VX_OK) return rc;
+  if ((rc = injected()) != VX_OK) return rc;
+  const int err = vx::launch_flash_fwd(args, stream);
+  if (err != 0) return fail(VX_ERR_LAUNCH, "flash attention launch failed (hipError_t %d)", err);
+  return ok();
+}
+
+int32_t vx_flash_attn_bias_check(const void* q, const void* k, const void* v, const void* out, const int32_t* kv_len,
+                                 const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride,
+                                 const float* bias, const int64_t* bias_strides, int32_t batch, int32_t seq_q,
+                                 int32_t seq_k, int32_t num_heads, int32_t head_dim, const int64_t* q_strides,
+                                 const int64_t* k_strides, const int64_t* v_strides, const int64_t* out_strides,
+                                 float scale) {
+  if (bias == nullptr) return fail(VX_ERR_INVALID_ARGUMENT, "bias must be non-NULL");
+  return flash_check(q, k, v, out, kv_len, key_valid, key_bias, key_mask_stride, batch, seq_q, seq_k, num_heads,
+                     head_dim, q_strides, k_strides, v_strides, out_strides, scale, nullptr, bias, bias_strides);
+}
+
+int32_t vx_flash_attn_bias_fwd(const void* q, const void* k, const void* v, void* out, const int32_t* kv_len,
+                               const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride,
+                               const float* bias, const int64_t* bias_strides, int32_t batch, int32_t seq_q,
+                               int32_t seq_k, int32_t num_heads, int32_t head_dim, const int64_t* q_strides,
+                               const int64_t* k_strides, const int64_t* v_strides, const int64_t* out_strides,
+                               float scale, void* stream) {
+  if (bias == nullptr) return fail(VX_ERR_INVALID_ARGUMENT, "bias must be non-NULL");
+  vx::FlashArgs args;
+  int32_t rc = flash_check(q, k, v, out, kv_len, key_valid, key_bias, key_mask_stride, batch, seq_q, seq_k,
+                           num_heads, head_dim, q_strides, k_strides, v_strides, out_strides, scale, &args, bias,
+                           bias_strides);
   if (rc != VX_OK) return rc;
   if ((rc = injected()) != VX_OK) return rc;
   const int err = vx::launch_flash_fwd(args, stream);

@@ -18,6 +18,8 @@ struct FlashArgs {
   const uint8_t* key_valid;  // [B, key_mask_stride] or nullptr
   const float* key_bias;     // [B, key_mask_stride] or nullptr
   int64_t key_mask_stride;   // elements between batch rows of the key masks
+  const float* full_bias;    // [b*fbs[0] + h*fbs[1] + q*fbs[2] + key] or nullptr
+  int64_t fbs[3];            // full-bias strides (elements) for batch, head, query
   int32_t B, Sq, Sk, H, D;
   int64_t qs[3], ks[3], vs[3], os[3];
   float scale;  // softmax scale (> 0)
