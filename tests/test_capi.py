@@ -60,7 +60,7 @@ def test_flash_check_accepts_valid_arguments():
     (dict(B=0), _lib.VX_ERR_INVALID_ARGUMENT, ">= 1"),
     (dict(Sk=0), _lib.VX_ERR_INVALID_ARGUMENT, ">= 1"),
     (dict(H=70000), _lib.VX_ERR_INVALID_ARGUMENT, "65535"),
-    (dict(D=64), _lib.VX_ERR_UNSUPPORTED, "head_dim"),
+    (dict(D=96), _lib.VX_ERR_UNSUPPORTED, "head_dim"),
     (dict(scale=0.0), _lib.VX_ERR_INVALID_ARGUMENT, "scale"),
     (dict(scale=float("inf")), _lib.VX_ERR_INVALID_ARGUMENT, "scale"),
     (dict(scale=-1.0), _lib.VX_ERR_INVALID_ARGUMENT, "scale"),
@@ -137,7 +137,7 @@ def test_error_injection_short_circuits_launch():
 def test_error_message_is_thread_local():
     import threading
     L = _lib.lib()
-    assert _flash_check(D=64) == _lib.VX_ERR_UNSUPPORTED
+    assert _flash_check(D=96) == _lib.VX_ERR_UNSUPPORTED
     seen = {}
 
     def other():
@@ -151,7 +151,7 @@ def test_error_message_is_thread_local():
 
 def test_raise_for_maps_codes():
     _lib.raise_for(_lib.VX_OK)
-    _flash_check(D=64)
+    _flash_check(D=96)
     with pytest.raises(NotImplementedError):
         _lib.raise_for(_lib.VX_ERR_UNSUPPORTED)
     _flash_check(B=0)
@@ -219,4 +219,5 @@ def test_flash_bias_check():
     assert _bias_check(strides=(0, 256, 258)) == _lib.VX_ERR_INVALID_ARGUMENT
     assert "multiple of 4" in _lib.last_error()
     assert _bias_check(strides=None) == _lib.VX_ERR_INVALID_ARGUMENT
-    assert _bias_check(D=64) == _lib.VX_ERR_UNSUPPORTED
+    assert _bias_check(D=64) == _lib.VX_OK
+    assert _bias_check(D=96) == _lib.VX_ERR_UNSUPPORTED

@@ -286,3 +286,44 @@ def test_flash_full_bias_and_masks(gpu, B, Sq, Sk, H, seed, kind):
         ref = O.attention(q, k, v, bias=bias + np.where(valid, 0.0, -np.inf))
     torch.cuda.synchronize()
     _check(out, ref, kind)
+
+
+# ------------------------------------------------------------ head dim 64
+D64_CASES = [
+    # B, Sq, Sk, H, seed, mask
+    (1, 128, 128, 2, 70, None),
+    (2, 200, 300, 3, 71, None),
+    (2, 130, 512, 4, 72, ("kv_len", 20, 512)),
+    (2, 96, 515, 2, 73, ("tail_pad", 0, 200)),
+]
+
+
+@pytest.mark.parametrize("B,Sq,Sk,H,seed,mask", D64_CASES)
+def test_flash_head_dim_64(gpu, B, Sq, Sk, H, seed, mask):
+    from vidax_amd import flash_attention
+    _say(f"flash D=64 B={B} Sq={Sq} Sk={Sk} H={H} seed={seed} mask={mask}")
+    q, k, v, extra = O.make_flash_inputs(B, Sq, Sk, H, 64, seed, mask)
+    kw = {key: torch.from_numpy(val).to(gpu) for key, val in extra.items()}
+    out = flash_attention(_t(q, gpu), _t(k, gpu), _t(v, gpu), **kw)
+    torch.cuda.synchronize()
+    _check(out, O.attention(q, k, v, kv_len=extra.get("kv_len"), key_valid=extra.get("key_valid")), "D=64")
+
+
+def test_flash_t5_relative_bias_head_dim_64(gpu):
+    """UMT5 encoder attention (src/vidax/models/wan/common/t5.py:40-68): head
+    dim 64, no softmax scaling, a learned (1, H, L, L) relative-position bias
+    plus a (B, 1, 1, L) padding mask, through dot_product_attention."""
+    from vidax_amd import dot_product_attention
+    _say("flash T5 D=64 L=512 H=8 with relative bias and padding")
+    B, L, H = 2, 512, 8
+    q, k, v, _ = O.make_flash_inputs(B, L, L, H, 64, 74)
+    q, k = q * 0.125, k  # T5 logits are O(1) after its learned projections
+    rng = np.random.default_rng(75)
+    pos_bias = rng.standard_normal((1, H, L, L)).astype(np.float32)
+    pad = np.zeros((B, 1, 1, L), np.float32)
+    pad[1, ..., 300:] = -np.inf
+    bias = pos_bias + pad
+    out = dot_product_attention(_t(q, gpu), _t(k, gpu), _t(v, gpu), bias=torch.from_numpy(bias).to(gpu),
+                                scale=1.0)
+    torch.cuda.synchronize()
+    _check(out, O.attention(O.bf16_round(q), k, v, scale=1.0, bias=bias), "t5")

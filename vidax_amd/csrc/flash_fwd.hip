@@ -33,35 +33,47 @@
 namespace vx {
 namespace {
 
-constexpr int kD = 128;
 constexpr int kBN = 64;                       // keys per tile
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kQueriesPerBlock = kWaves * 32;
-constexpr int kRowBytes = kD * 2;             // one bf16 key row
-constexpr int kTileBytes = kBN * kRowBytes;   // 16 KiB
-constexpr int kVBuf = 0;                      // three V tiles
-constexpr int kKBuf = 3 * kTileBytes;         // three K tiles
-constexpr int kSmemBytes = 6 * kTileBytes;    // 96 KiB
+
+// Per head dim (128 or 64): LDS rows, tiles, buffers and DMA copies.
+template <int D>
+struct FCfg {
+  static constexpr int kRowBytes = D * 2;               // one bf16 key row
+  static constexpr int kTileBytes = kBN * kRowBytes;    // 16 (8) KiB
+  static constexpr int kVBuf = 0;                       // three V tiles
+  static constexpr int kKBuf = 3 * kTileBytes;          // three K tiles
+  static constexpr int kSmemBytes = 6 * kTileBytes;     // 96 (48) KiB
+  static constexpr int kMaskBuf = 6 * kTileBytes;       // then the mask ring
+  static constexpr int kKeysPerCopy = 1024 / kRowBytes; // rows per 1 KiB DMA copy
+  static constexpr int kChunks = kRowBytes / 16;        // 16-byte chunks per row
+  static constexpr int kLoadsPerWave = kTileBytes / (kWaves * 1024);  // copies per wave per tile
+  static constexpr int kDB = D / 32;                    // 32-wide d blocks of O
+  static constexpr int kDS = D / 16;                    // 16-deep d steps of QK^T
+  static constexpr int kPV = 2 * 2 * kDB;               // MFMAs of PV per tile
+  static constexpr int kQK = 2 * kDS;                   // MFMAs of QK^T per tile
+  static constexpr int kSlots = kPV + kQK;              // 32 (16)
+  static constexpr int kScoresPerSlot = 32 / kSlots;    // 1 (2)
+};
 // Key masks of the masked variants go through LDS like K: a ring of 4 slots
 // of 320 bytes (64 validity bytes, then 64 fp32 biases), slot j % 4 holding
 // tile j's mask, staged by wave 0 together with K_j.
-constexpr int kMaskBuf = 6 * kTileBytes;
 constexpr int kMaskSlot = 320;
 constexpr int kMaskRing = 4;
 // Mask kinds (template argument, bits): validity bytes per key, additive bias
 // per key, additive bias per (query, key) of each head (read per query row
 // straight from global memory: meant for the short sequences that use it).
 constexpr int kMaskNone = 0, kMaskValid = 1, kMaskBias = 2, kMaskFull = 4;
-constexpr int kLoadsPerWave = (kBN / 4) / kWaves;  // 1 KiB wave loads per tile
 constexpr float kRescaleSlack = 8.0f;         // log2 units
 constexpr float kSumLimit = 256.0f;           // 2^kRescaleSlack
 constexpr float kNegBig = -1.0e30f;           // finite "no key seen yet" max
 
-// XOR swizzle of the 16-byte chunk index within a 256-byte LDS row. Eight
-// consecutive rows map one chunk to eight distinct 16-byte bank groups (the
-// ds_read_b128 K reads), and rows 4i..4i+3 map a chunk pair to four distinct
-// pairs (the transpose reads of V).
+// XOR swizzle of the 16-byte chunk index (low 3 bits) within an LDS row.
+// Eight consecutive rows map one chunk to eight distinct 16-byte bank groups
+// (the ds_read_b128 K reads), and rows 4i..4i+3 map a chunk pair to four
+// distinct pairs (the transpose reads of V).
 __device__ __forceinline__ int row_swizzle(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
 typedef VX_LDS unsigned char lds_u8;
@@ -89,9 +101,13 @@ __device__ __forceinline__ void wait_vmem() {
 // NaN test on the bit pattern (stays exact when the compiler may assume no NaNs).
 __device__ __forceinline__ bool is_nan_bits(float x) { return (__float_as_uint(x) & 0x7fffffffu) > 0x7f800000u; }
 
-template <int MASK>
+template <int MASK, int D>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_fwd_kernel(const FlashArgs a) {
+  using C = FCfg<D>;
+  constexpr int kRowBytes = C::kRowBytes, kTileBytes = C::kTileBytes, kVBuf = C::kVBuf, kKBuf = C::kKBuf;
+  constexpr int kSmemBytes = C::kSmemBytes, kMaskBuf = C::kMaskBuf, kLoadsPerWave = C::kLoadsPerWave;
+  constexpr int kDB = C::kDB, kDS = C::kDS, kPV = C::kPV, kSlots = C::kSlots;
   constexpr bool MASKED = MASK != kMaskNone;
   constexpr int kMaskCopies = (MASK & kMaskValid ? 1 : 0) + (MASK & kMaskBias ? 1 : 0);
   constexpr bool kFull = (MASK & kMaskFull) != 0;
@@ -118,12 +134,12 @@ void flash_fwd_kernel(const FlashArgs a) {
   const float c = a.scale * kLog2e;
 
   // ---- Q (B operand of S^T = K Q^T), resident for the whole key loop.
-  bf16x8 qr[8];
+  bf16x8 qr[kDS];
   {
     const int qi = min(qw0 + col, a.Sq - 1);
     const bf16* p = qg + (int64_t)qi * a.qs[1] + hf * 8;
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
+    for (int ds = 0; ds < kDS; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
   }
 
   // ---- per-lane LDS byte offsets inside one tile.
@@ -141,14 +157,16 @@ void flash_fwd_kernel(const FlashArgs a) {
 #pragma unroll
   for (int db1 = 0; db1 < 2; ++db1)
     voff[db1] = (hf * 4 + vr) * kRowBytes + (((4 * db1 + 2 * dh + (vc >> 1)) ^ vsw) * 16) + (vc & 1) * 8;
-  // staging: this lane's row within its 4-row group and its 16-byte column
-  const int srow = lane >> 4;
-  const int scol = lane & 15;
+  // staging: this lane's row within its group of kKeysPerCopy rows and its
+  // 16-byte column
+  const int srow = lane / C::kChunks;
+  const int scol = lane % C::kChunks;
 
   // ---- global -> LDS staging of one 64-key tile on the LDS DMA path
-  // (global_load_lds_dwordx4): each wave instruction fills 4 consecutive
-  // 256-byte rows, lane L landing at byte 16*L, so lane L fetches the global
-  // chunk that the swizzle places there. kLoadsPerWave instructions per tile.
+  // (global_load_lds_dwordx4): each wave instruction fills kKeysPerCopy
+  // consecutive rows (1 KiB), lane L landing at byte 16*L, so lane L fetches
+  // the global chunk that the swizzle places there. kLoadsPerWave
+  // instructions per wave per tile.
   // Tiles that lie wholly below kv_end add a uniform tile offset to per-lane
   // row pointers computed once; the tail tile clamps its rows to kv_end - 1.
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
@@ -156,7 +174,7 @@ void flash_fwd_kernel(const FlashArgs a) {
   const bf16* vlane[kLoadsPerWave];
 #pragma unroll
   for (int p = 0; p < kLoadsPerWave; ++p) {
-    const int r = (wave * kLoadsPerWave + p) * 4 + srow;
+    const int r = (wave * kLoadsPerWave + p) * C::kKeysPerCopy + srow;
     klane[p] = kg + (int64_t)r * a.ks[1] + ((scol ^ row_swizzle(r)) * 8);
     vlane[p] = vg + (int64_t)r * a.vs[1] + ((scol ^ row_swizzle(r)) * 8);
   }
@@ -166,11 +184,11 @@ void flash_fwd_kernel(const FlashArgs a) {
       const int64_t off = (int64_t)(t * kBN) * sstride;
 #pragma unroll
       for (int p = 0; p < kLoadsPerWave; ++p)
-        lds_dma16(lanep[p] + off, lds_base + buf_off + (wave * kLoadsPerWave + p) * 4 * kRowBytes);
+        lds_dma16(lanep[p] + off, lds_base + buf_off + (wave * kLoadsPerWave + p) * C::kKeysPerCopy * kRowBytes);
     } else {
 #pragma unroll
       for (int p = 0; p < kLoadsPerWave; ++p) {
-        const int r0 = (wave * kLoadsPerWave + p) * 4;
+        const int r0 = (wave * kLoadsPerWave + p) * C::kKeysPerCopy;
         const int r = r0 + srow;
         const int key = min(t * kBN + r, kv_end - 1);
         const bf16* src = base + (int64_t)key * sstride + ((scol ^ row_swizzle(r)) * 8);
@@ -184,7 +202,7 @@ void flash_fwd_kernel(const FlashArgs a) {
     S[1] = f32x16{};
     const lds_u8* kb0 = lds + buf_off;
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) {
+    for (int ds = 0; ds < kDS; ++ds) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const bf16x8 kf = *(const VX_LDS bf16x8*)(kb0 + koff[ds & 3] + kb * 32 * kRowBytes + (ds >> 2) * 128);
@@ -192,14 +210,14 @@ void flash_fwd_kernel(const FlashArgs a) {
       }
     }
   };
-  auto pv = [&](int buf_off, const bf16x8 (&P)[2][2], f32x16 (&O)[4]) {
+  auto pv = [&](int buf_off, const bf16x8 (&P)[2][2], f32x16 (&O)[kDB]) {
     const lds_u8* vb = lds + buf_off;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
+        for (int db = 0; db < kDB; ++db) {
           const lds_u8* p = vb + voff[db & 1] + (kb * 32 + 16 * j) * kRowBytes + (db >> 1) * 128;
           const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p);
           const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + 8 * kRowBytes));
@@ -225,9 +243,9 @@ void flash_fwd_kernel(const FlashArgs a) {
     return l;
   };
 
-  f32x16 O[4];
+  f32x16 O[kDB];
 #pragma unroll
-  for (int db = 0; db < 4; ++db) O[db] = f32x16{};
+  for (int db = 0; db < kDB; ++db) O[db] = f32x16{};
   float m_run = kNegBig, l_run = 0.f;
 
   const uint8_t* vrow = (MASK & kMaskValid) ? a.key_valid + (int64_t)b * a.key_mask_stride : nullptr;
@@ -359,38 +377,44 @@ void flash_fwd_kernel(const FlashArgs a) {
       {
         const lds_u8* kb0 = lds + kKBuf + kb_cur * kTileBytes;
         const lds_u8* vb0 = lds + kVBuf + vb_prev * kTileBytes;
+        // slot s < kPV: PV fragment (kb, j, db) with s = (kb * 2 + j) * kDB + db;
+        // slot s >= kPV: QK^T fragment (ds, kb) with s - kPV = 2 * ds + kb.
         auto frag = [&](int s) -> bf16x8 {
-          if (s < 16) {
-            const int kb = s >> 3, j = (s >> 2) & 1, db = s & 3;
+          if (s < kPV) {
+            const int db = s % kDB, j = (s / kDB) & 1, kb = s / (2 * kDB);
             const lds_u8* p = vb0 + voff[db & 1] + (kb * 32 + 16 * j) * kRowBytes + (db >> 1) * 128;
             const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p);
             const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + 8 * kRowBytes));
             return concat(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi));
           }
-          const int ds = (s - 16) >> 1, kb = (s - 16) & 1;
+          const int ds = (s - kPV) >> 1, kb = (s - kPV) & 1;
           return *(const VX_LDS bf16x8*)(kb0 + koff[ds & 3] + kb * 32 * kRowBytes + (ds >> 2) * 128);
         };
         const float mneg = -m_run;
         const bf16x2 one2 = {(bf16)1.0f, (bf16)1.0f};
-        bf16x8 fr[32];
+        bf16x8 fr[kSlots];
         float pf[32];
         bf16x2 pk[16];
         fr[0] = frag(0);
         fr[1] = frag(1);
 #pragma unroll
-        for (int s = 0; s < 32; ++s) {
-          if (s + 2 < 32) fr[s + 2] = frag(s + 2);
-          if (s < 16) {
-            const int kb = s >> 3, j = (s >> 2) & 1, db = s & 3;
+        for (int s = 0; s < kSlots; ++s) {
+          if (s + 2 < kSlots) fr[s + 2] = frag(s + 2);
+          if (s < kPV) {
+            const int db = s % kDB, j = (s / kDB) & 1, kb = s / (2 * kDB);
             O[db] = mfma32x32x16(fr[s], Pp[kb][j], O[db]);
           } else {
-            const int ds = (s - 16) >> 1, kb = (s - 16) & 1;
+            const int ds = (s - kPV) >> 1, kb = (s - kPV) & 1;
             Sn[kb] = mfma32x32x16(fr[s], qr[ds], Sn[kb]);
           }
-          pf[s] = fast_exp2(__builtin_fmaf(S[s >> 4][s & 15], cc, mneg));
-          if (s & 1) {
-            pk[s >> 1] = bf16x2{(bf16)pf[s - 1], (bf16)pf[s]};
-            l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[s >> 1], one2, l_tile, false);
+#pragma unroll
+          for (int u = 0; u < C::kScoresPerSlot; ++u) {
+            const int e = s * C::kScoresPerSlot + u;  // score e of the lane's 32
+            pf[e] = fast_exp2(__builtin_fmaf(S[e >> 4][e & 15], cc, mneg));
+            if (e & 1) {
+              pk[e >> 1] = bf16x2{(bf16)pf[e - 1], (bf16)pf[e]};
+              l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[e >> 1], one2, l_tile, false);
+            }
           }
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -418,7 +442,7 @@ void flash_fwd_kernel(const FlashArgs a) {
         m_run = mn;
         l_run *= alpha;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) O[db] *= alpha;
+        for (int db = 0; db < kDB; ++db) O[db] *= alpha;
         l_tile = probs(S, cc, m_run, P);
       }
       l_run += l_tile;
@@ -453,7 +477,7 @@ void flash_fwd_kernel(const FlashArgs a) {
   if (qi < a.Sq) {
     bf16* orow = og + (int64_t)qi * a.os[1];
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < kDB; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         bf16x4 ov;
@@ -467,13 +491,17 @@ void flash_fwd_kernel(const FlashArgs a) {
 template <int MASK>
 int launch(const FlashArgs& a, hipStream_t stream) {
   dim3 grid((a.Sq + kQueriesPerBlock - 1) / kQueriesPerBlock, a.H, a.B);
-  hipLaunchKernelGGL((flash_fwd_kernel<MASK>), grid, dim3(kThreads), 0, stream, a);
+  if (a.D == 64)
+    hipLaunchKernelGGL((flash_fwd_kernel<MASK, 64>), grid, dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((flash_fwd_kernel<MASK, 128>), grid, dim3(kThreads), 0, stream, a);
   return (int)hipGetLastError();
 }
 
 }  // namespace
 
 int launch_flash_fwd(const FlashArgs& a, void* stream) {
+  if (a.D != 128 && a.D != 64) return (int)hipErrorNotSupported;
   hipStream_t s = (hipStream_t)stream;
   const int mask = (a.key_valid != nullptr ? kMaskValid : 0) | (a.key_bias != nullptr ? kMaskBias : 0);
   if (a.full_bias != nullptr) {

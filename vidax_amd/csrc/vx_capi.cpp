@@ -73,7 +73,8 @@ int32_t flash_check(const void* q, const void* k, const void* v, const void* out
                 Sk, H);
   if (B > 65535 || H > 65535)
     return fail(VX_ERR_INVALID_ARGUMENT, "batch (%d) and num_heads (%d) must be <= 65535", B, H);
-  if (D != 128) return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 128)", D);
+  if (D != 128 && D != 64)
+    return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 64 and 128)", D);
   if (!(scale > 0.f) || !std::isfinite(scale))
     return fail(VX_ERR_INVALID_ARGUMENT, "scale must be positive and finite (got %g)", (double)scale);
   if (key_valid != nullptr || key_bias != nullptr) {
