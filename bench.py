@@ -222,7 +222,8 @@ def main(argv=None):
 
         def step():
             vidax_amd.flash_attention(q, k, v, out=out, **kw)
-        kernel_name = "flash_fwd_kernel<true>" if kw else "flash_fwd_kernel<false>"
+        mask_kind = (1 if "key_valid" in kw else 0) | (2 if "key_bias" in kw else 0)
+        kernel_name = f"flash_fwd_kernel<{mask_kind}, 128>"
     elif kind == "prologue":
         from vidax_amd.prologue import create_rope3d_freqs, qk_norm_rope
         g = torch.Generator(device=dev)
@@ -241,7 +242,7 @@ def main(argv=None):
         def step():
             qk_norm_rope(qx, wq, freqs, p["H"])
             qk_norm_rope(kx, wk, freqs, p["H"])
-        kernel_name = "qk_prologue_kernel<16>"
+        kernel_name = "qk_prologue_kernel<10, true>"
     else:
         g = torch.Generator(device=dev)
         g.manual_seed(p["seed"])

@@ -17,15 +17,15 @@ from . import _lib
 __all__ = ["neighborhood_attention_3d", "na3d_attention", "na3d_kernel_name"]
 
 
-def na3d_kernel_name(width: int, kernel_w: int) -> str:
+def na3d_kernel_name(width: int, kernel_w: int, head_dim: int = 128) -> str:
     """Name of the kernel the library launches for this x window (profiling aid):
     the pipelined row-streaming kernel with 16- or 32-key x segments up to
     kw' = 25, the per-wave kernel above that (kw' = min(kw, W))."""
     kw = min(int(kernel_w), int(width))
     if kw <= 9:
-        return "na3d_pipe_kernel<16>"
+        return f"na3d_pipe_kernel<16, {head_dim}>"
     if kw <= 25:
-        return "na3d_pipe_kernel<32>"
+        return f"na3d_pipe_kernel<32, {head_dim}>"
     return "na3d_wave_kernel"
 
 
