@@ -193,6 +193,33 @@ int32_t vx_rmsnorm_rope_check(const void* x, const void* out, const float* weigh
                               const int64_t* out_strides);
 
 /*
+ * vx_rmsnorm_rope_fwd with one more step between the norm and the rotation:
+ *   if post_scale != 1:  y = bf16(y * bf16(post_scale))
+ * (vx_rmsnorm_rope_fwd is this call with post_scale = 1). post_scale must be
+ * finite; all other arguments and limits are vx_rmsnorm_rope_fwd's.
+ *
+ * Replaces the q/k preparation of the LTX-2.5 diffusion-VAE neighbourhood
+ * attention block, src/vidax/models/ltx2_5/diffusion_vae.py:255-273: per-head
+ * RMSNorm (q_norm / k_norm, per_head_norm = 1), q * head_dim^-0.5 (a bf16
+ * array times a weakly typed scalar: the scalar is rounded to bf16), then the
+ * absolute interleaved-pair RoPE of _apply_abs_rope (:106-149) with per-token
+ * tables of the (T, H, W) split of _default_rope_dim_split (:96-103). The
+ * rows are the (B, T, H, W, NH, HD) tokens, seq = T * H * W.
+ */
+int32_t vx_rmsnorm_scale_rope_fwd(const void* x, void* out, const float* weight, float eps, int32_t per_head_norm,
+                                  float post_scale, const float* rope_cos, const float* rope_sin,
+                                  int64_t rope_stride, int32_t batch, int32_t seq, int32_t num_heads,
+                                  int32_t head_dim, const int64_t* x_strides, const int64_t* out_strides,
+                                  void* stream);
+
+/* Host-only argument check for vx_rmsnorm_scale_rope_fwd (no GPU needed). */
+int32_t vx_rmsnorm_scale_rope_check(const void* x, const void* out, const float* weight, float eps,
+                                    int32_t per_head_norm, float post_scale, const float* rope_cos,
+                                    const float* rope_sin, int64_t rope_stride, int32_t batch, int32_t seq,
+                                    int32_t num_heads, int32_t head_dim, const int64_t* x_strides,
+                                    const int64_t* out_strides);
+
+/*
  * Failure injection for error-path tests: while `code` is non-zero, every
  * vx_*_fwd call that passes argument checks returns `code` without launching,
  * with a message naming the injection. 0 turns it off. Process-wide.

@@ -32,7 +32,7 @@ def test_header_symbols_are_exported():
 
 
 def test_abi_version():
-    assert _lib.lib().vx_abi_version() == 10300
+    assert _lib.lib().vx_abi_version() == 10400
 
 
 def _flash_check(**kw):
@@ -198,6 +198,25 @@ def test_prologue_check_accepts_valid_arguments():
 def test_prologue_check_rejects(kw, code, frag):
     assert _prologue_check(**kw) == code
     assert frag in _lib.last_error()
+
+
+def _scaled_prologue_check(post_scale, **kw):
+    args = dict(x=A, out=A + 4096, w=A, eps=1e-6, per_head=1, cos=A, sin=A, tab=32, B=1, S=10, H=4, D=64)
+    args.update(kw)
+    return _lib.lib().vx_rmsnorm_scale_rope_check(
+        args["x"], args["out"], args["w"], ctypes.c_float(args["eps"]), args["per_head"], ctypes.c_float(post_scale),
+        args["cos"], args["sin"], args["tab"], args["B"], args["S"], args["H"], args["D"], None, None)
+
+
+def test_scaled_prologue_check():
+    assert _scaled_prologue_check(0.125) == _lib.VX_OK
+    assert _scaled_prologue_check(1.0) == _lib.VX_OK
+    assert _scaled_prologue_check(-2.0, w=None) == _lib.VX_OK
+    for bad in (float("inf"), float("nan")):
+        assert _scaled_prologue_check(bad) == _lib.VX_ERR_INVALID_ARGUMENT
+        assert "post_scale" in _lib.last_error()
+    # the shared checks still apply
+    assert _scaled_prologue_check(0.125, D=96) == _lib.VX_ERR_UNSUPPORTED
 
 
 def _bias_check(bias=A, strides=(0, 256 * 256, 256), **kw):

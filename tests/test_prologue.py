@@ -130,6 +130,100 @@ def test_planted_mistakes_are_caught():
     assert not np.array_equal(wrong, P.rms_norm(xx, np.ones(2, np.float32), eps=0.0))
 
 
+# ------------------------------------------- neighbourhood block (abs RoPE)
+def test_abs_rope_split_known_answers():
+    """(d_t, d_h, d_w): head_dim 40 takes the odd-half branch (d_t 10 -> 8)."""
+    assert P.default_rope_dim_split(64) == (16, 24, 24)
+    assert P.default_rope_dim_split(128) == (32, 48, 48)
+    assert P.default_rope_dim_split(96) == (24, 36, 36)
+    assert P.default_rope_dim_split(40) == (8, 16, 16)
+    assert P.default_rope_dim_split(32) == (8, 12, 12)
+
+
+def _complex_rotation(x, split, base=10000.0):
+    """float64 rotation written as complex multiplication: the pair
+    (x[2j], x[2j+1]) of axis chunk a is the number x[2j] + i x[2j+1], times
+    exp(i * pos_a * base^(-2j/d_a))."""
+    _, T, H, W, _, HD = x.shape
+    out = np.empty(x.shape, np.float64)
+    lo = 0
+    for axis, (d, n) in enumerate(zip(split, (T, H, W))):
+        z = x[..., lo:lo + d:2].astype(np.float64) + 1j * x[..., lo + 1:lo + d:2]
+        theta = np.arange(n)[:, None] * base ** (-np.arange(0, d, 2) / d)[None, :]
+        shape = [1, 1, 1, 1, 1, d // 2]
+        shape[axis + 1] = n
+        z = z * np.exp(1j * theta.reshape(shape))
+        out[..., lo:lo + d:2], out[..., lo + 1:lo + d:2] = z.real, z.imag
+        lo += d
+    return out
+
+
+@pytest.mark.parametrize("HD", [64, 128, 40])
+def test_abs_rope_matches_complex_rotation(HD):
+    """Pins the interleaved pairing, the sign of the rotation, the frequency
+    formula and which channels follow T, H and W."""
+    rng = np.random.default_rng(HD)
+    x = _bf16_normal(rng, (1, 3, 4, 5, 2, HD))
+    got = P.apply_abs_rope3d(x)
+    ref = _complex_rotation(x, P.default_rope_dim_split(HD))
+    assert np.max(np.abs(got - ref)) <= 2 ** -8 * np.max(np.abs(ref)) + 1e-6
+    # mistakes that must fail the same check
+    split = P.default_rope_dim_split(HD)
+    wrong_axes = _complex_rotation(x, split[::-1]) if split[0] != split[2] else None
+    if wrong_axes is not None:
+        assert np.max(np.abs(got - wrong_axes)) > 1e-2
+    neg = _complex_rotation(x[..., :], split)
+    neg[..., 1::2] = -_complex_rotation(x * np.where(np.arange(HD) % 2, -1, 1), split)[..., 1::2]
+    assert np.max(np.abs(got - neg)) > 1e-2  # the conjugate rotation
+
+
+def test_abs_rope_tables_equal_axis_form():
+    """The per-token tables (the kernel's input) applied pair by pair give
+    the same bits as the axis-by-axis form."""
+    rng = np.random.default_rng(5)
+    T, H, W, NH, HD = 3, 4, 6, 3, 64
+    x = _bf16_normal(rng, (2, T, H, W, NH, HD))
+    cos, sin = P.create_abs_rope3d_freqs(T, H, W, HD)
+    via_tables = P.apply_rope3d(x.reshape(2, T * H * W, NH, HD), cos, sin).reshape(x.shape)
+    np.testing.assert_array_equal(via_tables, P.apply_abs_rope3d(x))
+    # the origin token is not rotated; along W only the last 12 pairs turn
+    np.testing.assert_array_equal(cos[0], 1.0)
+    moved = np.abs(np.arctan2(sin, cos).reshape(T, H, W, 32)[0, 0, 1]) > 0
+    assert moved.tolist() == [False] * 20 + [True] * 12
+
+
+def test_abs_rope_relative_positions():
+    """q.k after rotation depends only on the offset along each axis."""
+    rng = np.random.default_rng(6)
+    T, H, W, HD = 5, 6, 7, 64
+    q = rng.standard_normal(HD)
+    k = rng.standard_normal(HD)
+    cos, sin = P.create_abs_rope3d_freqs(T, H, W, HD)
+
+    def rot(v, t, h, w):
+        i = (t * H + h) * W + w
+        c, s = cos[i].astype(np.float64), sin[i].astype(np.float64)
+        out = np.empty(HD)
+        out[0::2] = v[0::2] * c - v[1::2] * s
+        out[1::2] = v[0::2] * s + v[1::2] * c
+        return out
+
+    base = rot(q, 2, 3, 4) @ rot(k, 1, 1, 2)
+    assert abs(base - rot(q, 4, 5, 6) @ rot(k, 3, 3, 4)) < 1e-6 * (abs(base) + 1)  # fp32 tables
+    assert abs(base - rot(q, 2, 3, 5) @ rot(k, 1, 1, 2)) > 1e-4
+
+
+def test_post_scale_known_answers():
+    """q * head_dim^-0.5 in bf16: the scalar is rounded to bf16 first
+    (128^-0.5 -> 0.08837890625); 64^-0.5 = 0.125 is exact."""
+    y = np.array([[1.0, 3.0, -0.5, 1.5]], np.float32).reshape(1, 1, 1, 1, 1, 4)
+    out = P.na3d_qk_norm_rope(y, None, post_scale=128 ** -0.5, rope=False)
+    np.testing.assert_array_equal(out.ravel(), A.bf16_round(y.ravel() * np.float32(0.08837890625)))
+    assert A.bf16_round(np.float32(128 ** -0.5)) == np.float32(0.08837890625)
+    out = P.na3d_qk_norm_rope(y, None, post_scale=0.125, rope=False)
+    np.testing.assert_array_equal(out.ravel(), y.ravel() / 8)
+
+
 # ------------------------------------------------------------------ GPU
 def _ulps(got, ref):
     ref = np.asarray(ref, np.float64)
@@ -237,3 +331,43 @@ def test_unsupported_rows_raise(gpu):
     x = torch.zeros((1, 4, 72 * 128), dtype=torch.bfloat16, device=gpu)
     with pytest.raises(NotImplementedError):
         qk_norm_rope(x, None, None, 72)
+
+
+NA_PROLOGUE_CASES = [
+    # (B, (T, H, W), NH, HD, norm, post_scale, rope)
+    (1, (3, 5, 7), 4, 64, True, 64 ** -0.5, True),     # LTX-2.5 q: head_dim 64
+    (2, (2, 4, 6), 4, 64, True, 1.0, True),            # k: no scale
+    (1, (3, 4, 9), 8, 128, True, 128 ** -0.5, True),   # head_dim 128
+    (1, (2, 3, 5), 6, 64, False, 1.0, True),           # rope only
+    (1, (2, 3, 5), 2, 128, True, 0.7, False),          # norm and scale only
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,grid,NH,HD,norm,post,rope", NA_PROLOGUE_CASES)
+def test_na3d_qk_norm_rope_matches_oracle(gpu, B, grid, NH, HD, norm, post, rope):
+    from vidax_amd import create_abs_rope3d_freqs, na3d_qk_norm_rope
+    print(f"[case] na3d_qk_norm_rope B={B} grid={grid} NH={NH} HD={HD} norm={norm} post={post:.4f} rope={rope}",
+          flush=True)
+    rng = np.random.default_rng(sum(grid) * NH + HD)
+    x = _bf16_normal(rng, (B, *grid, NH, HD), 2.0)
+    w = (1.0 + 0.5 * rng.standard_normal(HD)).astype(np.float32) if norm else None
+    ref = P.na3d_qk_norm_rope(x, w, post_scale=post, rope=rope)
+    freqs = create_abs_rope3d_freqs(*grid, HD, device=gpu) if rope else None
+    out = na3d_qk_norm_rope(_dev(x, gpu), torch.from_numpy(w).to(gpu) if norm else None, freqs, post_scale=post)
+    torch.cuda.synchronize()
+    _check(out.float().cpu().numpy(), ref, "na3d_qk_norm_rope")
+
+
+@pytest.mark.gpu
+def test_abs_rope_tables_and_apply_match_oracle(gpu):
+    from vidax_amd import apply_abs_rope3d, create_abs_rope3d_freqs
+    cos, sin = create_abs_rope3d_freqs(4, 6, 9, 64, device=gpu)
+    rc, rs = P.create_abs_rope3d_freqs(4, 6, 9, 64)
+    np.testing.assert_allclose(cos.reshape(-1, 32).cpu().numpy(), rc, atol=2e-6)
+    np.testing.assert_allclose(sin.reshape(-1, 32).cpu().numpy(), rs, atol=2e-6)
+    rng = np.random.default_rng(12)
+    x = _bf16_normal(rng, (1, 4, 6, 9, 3, 64))
+    out = apply_abs_rope3d(_dev(x, gpu), (cos, sin))
+    torch.cuda.synchronize()
+    _check(out.float().cpu().numpy(), P.apply_abs_rope3d(x), "apply_abs_rope3d")

@@ -31,6 +31,8 @@ EXPORTED_SYMBOLS = (
     "vx_rmsnorm_rope_check",
     "vx_flash_attn_bias_fwd",
     "vx_flash_attn_bias_check",
+    "vx_rmsnorm_scale_rope_fwd",
+    "vx_rmsnorm_scale_rope_check",
 )
 
 _lock = threading.Lock()
@@ -48,6 +50,7 @@ _NA3D_ARGS = [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i
 _FLASH_BIAS_ARGS = [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64p, _i32, _i32, _i32, _i32, _i32,
                     _i64p, _i64p, _i64p, _i64p, _f32]
 _PROLOGUE_ARGS = [_p, _p, _p, _f32, _i32, _p, _p, _i64, _i32, _i32, _i32, _i32, _i64p, _i64p]
+_SCALED_PROLOGUE_ARGS = _PROLOGUE_ARGS[:5] + [_f32] + _PROLOGUE_ARGS[5:]
 
 
 class VxError(RuntimeError):
@@ -92,6 +95,10 @@ def lib() -> ctypes.CDLL:
             h.vx_rmsnorm_rope_fwd.argtypes = _PROLOGUE_ARGS + [_p]
             h.vx_rmsnorm_rope_check.restype = _i32
             h.vx_rmsnorm_rope_check.argtypes = _PROLOGUE_ARGS
+            h.vx_rmsnorm_scale_rope_fwd.restype = _i32
+            h.vx_rmsnorm_scale_rope_fwd.argtypes = _SCALED_PROLOGUE_ARGS + [_p]
+            h.vx_rmsnorm_scale_rope_check.restype = _i32
+            h.vx_rmsnorm_scale_rope_check.argtypes = _SCALED_PROLOGUE_ARGS
             h.vx_debug_inject_error.restype = None
             h.vx_debug_inject_error.argtypes = [_i32]
             _lib = h

@@ -6,11 +6,14 @@
 //   norm:  y = bf16( bf16(x * rsqrt(mean(x^2) + eps)) * bf16(w) )
 //          mean over the whole row (group = row) or over each head (group =
 //          head_dim); fp32 statistics. Skipped when no weight is given.
+//   scale: y = bf16(y * bf16(post_scale)), skipped when post_scale is 1
+//          (the neighbourhood-attention block's q * head_dim^-0.5).
 //   rope:  adjacent pairs (y[2j], y[2j+1]) of every head are rotated by the
 //          token's (cos[j], sin[j]) in fp32 and rounded to bf16. Skipped when
 //          no tables are given.
 // These are the dtype points of the reference's RMSNorm (normalise in fp32,
-// cast, multiply by the cast weight) and apply_rope3d (fp32 rotation, cast).
+// cast, multiply by the cast weight), a bf16 array times a weakly typed
+// scalar, and the fp32 rotations of apply_rope3d / _apply_abs_rope (cast back).
 //
 // Layout: row s of batch b starts at x + b*x_bstride + s*x_sstride (elements)
 // and is contiguous; lane l of the wave owns the 16-byte chunks l, l + 64, ...
@@ -91,6 +94,17 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const 
           const float w = (float)to_bf16(e < 4 ? w0[e] : w1[e - 4]);
           v[i][e] = to_bf16(n * w);
         }
+      }
+    }
+  }
+
+  if (a.post_scale != 1.0f) {
+    const float ps = (float)to_bf16(a.post_scale);
+#pragma unroll
+    for (int i = 0; i < NCHUNK; ++i) {
+      if (live(lane + 64 * i)) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[i][e] = to_bf16((float)v[i][e] * ps);
       }
     }
   }

@@ -181,9 +181,12 @@ int32_t na3d_check(const void* q, const void* k, const void* v, const void* out,
 }
 
 int32_t prologue_check(const void* x, const void* out, const float* weight, float eps, int32_t per_head,
-                       const float* rope_cos, const float* rope_sin, int64_t rope_stride, int32_t B, int32_t S,
-                       int32_t H, int32_t D, const int64_t* xs_in, const int64_t* os_in, vx::PrologueArgs* args) {
+                       float post_scale, const float* rope_cos, const float* rope_sin, int64_t rope_stride,
+                       int32_t B, int32_t S, int32_t H, int32_t D, const int64_t* xs_in, const int64_t* os_in,
+                       vx::PrologueArgs* args) {
   if (x == nullptr || out == nullptr) return fail(VX_ERR_INVALID_ARGUMENT, "x and out must be non-NULL");
+  if (!std::isfinite(post_scale))
+    return fail(VX_ERR_INVALID_ARGUMENT, "post_scale must be finite (got %g)", (double)post_scale);
   if (!aligned16(x) || !aligned16(out)) return fail(VX_ERR_INVALID_ARGUMENT, "x and out must be 16-byte aligned");
   if (B < 1 || S < 1 || H < 1)
     return fail(VX_ERR_INVALID_ARGUMENT, "batch (%d), seq (%d) and num_heads (%d) must be >= 1", B, S, H);
@@ -224,6 +227,7 @@ int32_t prologue_check(const void* x, const void* out, const float* weight, floa
     args->cos = rope_cos;
     args->sin = rope_sin;
     args->eps = eps;
+    args->post_scale = post_scale;
     args->per_head = per_head;
     args->B = B;
     args->S = S;
@@ -248,7 +252,7 @@ int32_t injected() {
 
 extern "C" {
 
-int32_t vx_abi_version(void) { return 10300; }
+int32_t vx_abi_version(void) { return 10400; }
 
 const char* vx_last_error(void) { return g_error; }
 
@@ -333,17 +337,35 @@ int32_t vx_rmsnorm_rope_check(const void* x, const void* out, const float* weigh
                               const float* rope_cos, const float* rope_sin, int64_t rope_stride, int32_t batch,
                               int32_t seq, int32_t num_heads, int32_t head_dim, const int64_t* x_strides,
                               const int64_t* out_strides) {
-  return prologue_check(x, out, weight, eps, per_head_norm, rope_cos, rope_sin, rope_stride, batch, seq, num_heads,
-                        head_dim, x_strides, out_strides, nullptr);
+  return prologue_check(x, out, weight, eps, per_head_norm, 1.0f, rope_cos, rope_sin, rope_stride, batch, seq,
+                        num_heads, head_dim, x_strides, out_strides, nullptr);
 }
 
 int32_t vx_rmsnorm_rope_fwd(const void* x, void* out, const float* weight, float eps, int32_t per_head_norm,
                             const float* rope_cos, const float* rope_sin, int64_t rope_stride, int32_t batch,
                             int32_t seq, int32_t num_heads, int32_t head_dim, const int64_t* x_strides,
                             const int64_t* out_strides, void* stream) {
+  return vx_rmsnorm_scale_rope_fwd(x, out, weight, eps, per_head_norm, 1.0f, rope_cos, rope_sin, rope_stride, batch,
+                                   seq, num_heads, head_dim, x_strides, out_strides, stream);
+}
+
+int32_t vx_rmsnorm_scale_rope_check(const void* x, const void* out, const float* weight, float eps,
+                                    int32_t per_head_norm, float post_scale, const float* rope_cos,
+                                    const float* rope_sin, int64_t rope_stride, int32_t batch, int32_t seq,
+                                    int32_t num_heads, int32_t head_dim, const int64_t* x_strides,
+                                    const int64_t* out_strides) {
+  return prologue_check(x, out, weight, eps, per_head_norm, post_scale, rope_cos, rope_sin, rope_stride, batch, seq,
+                        num_heads, head_dim, x_strides, out_strides, nullptr);
+}
+
+int32_t vx_rmsnorm_scale_rope_fwd(const void* x, void* out, const float* weight, float eps, int32_t per_head_norm,
+                                  float post_scale, const float* rope_cos, const float* rope_sin,
+                                  int64_t rope_stride, int32_t batch, int32_t seq, int32_t num_heads,
+                                  int32_t head_dim, const int64_t* x_strides, const int64_t* out_strides,
+                                  void* stream) {
   vx::PrologueArgs args;
-  int32_t rc = prologue_check(x, out, weight, eps, per_head_norm, rope_cos, rope_sin, rope_stride, batch, seq,
-                              num_heads, head_dim, x_strides, out_strides, &args);
+  int32_t rc = prologue_check(x, out, weight, eps, per_head_norm, post_scale, rope_cos, rope_sin, rope_stride, batch,
+                              seq, num_heads, head_dim, x_strides, out_strides, &args);
   if (rc != VX_OK) return rc;
   if ((rc = injected()) != VX_OK) return rc;
   const int err = vx::launch_qk_prologue(args, stream);

@@ -44,6 +44,7 @@ struct PrologueArgs {
   const float* cos;     // (S, >= D/2) rows at tab_stride; NULL = no rotation
   const float* sin;
   float eps;
+  float post_scale;     // 1: none; else y = bf16(y * bf16(post_scale)) after the norm
   int32_t per_head;     // 0: mean over the whole row, 1: over each head
   int32_t B, S, H, D;
   int64_t x_bstride, x_sstride, o_bstride, o_sstride, tab_stride;  // elements

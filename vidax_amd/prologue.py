@@ -3,10 +3,13 @@
 Mirrors the reference's q/k preparation in the DiT attention block:
 `RMSNorm` (`src/vidax/core/attention.py:149-161`), `create_rope3d_freqs` and
 `apply_rope3d` (`src/vidax/core/rope3d.py:45-111`), as used by Wan's `attend`
-(`src/vidax/models/wan/common/dit_layers.py:135-149`). The norm and the
-rotation run in one HIP kernel (`vx_rmsnorm_rope_fwd`) that reads each bf16
-row once and writes it once; `qk_norm_rope` is the fused form of the
-reference's norm -> reshape -> rope sequence.
+(`src/vidax/models/wan/common/dit_layers.py:135-149`), and the LTX-2.5
+diffusion-VAE neighbourhood block's per-head norm, q scaling and absolute
+RoPE (`src/vidax/models/ltx2_5/diffusion_vae.py:96-149,255-273`). The norm,
+the scaling and the rotation run in one HIP kernel
+(`vx_rmsnorm_scale_rope_fwd`) that reads each bf16 row once and writes it
+once; `qk_norm_rope` and `na3d_qk_norm_rope` are the fused forms of the
+reference's norm -> (scale) -> rope sequences.
 """
 from __future__ import annotations
 
@@ -17,7 +20,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["create_rope3d_freqs", "apply_rope3d", "rms_norm", "qk_norm_rope"]
+__all__ = ["create_rope3d_freqs", "apply_rope3d", "rms_norm", "qk_norm_rope",
+           "default_rope_dim_split", "create_abs_rope3d_freqs", "apply_abs_rope3d", "na3d_qk_norm_rope"]
 
 
 def _axis_freqs(seq_len: int, dim: int, theta: float, device) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -74,7 +78,7 @@ def _tables(freqs, seq: int, half: int, device) -> Tuple[torch.Tensor, torch.Ten
 
 
 def _run(x4: torch.Tensor, out4: torch.Tensor, weight: Optional[torch.Tensor], eps: float, per_head: bool,
-         tables) -> None:
+         tables, post_scale: float = 1.0) -> None:
     B, S, H, D = x4.shape
     if x4.stride(3) != 1 or x4.stride(2) != D:
         raise ValueError("each token row (num_heads * head_dim) must be contiguous")
@@ -86,10 +90,10 @@ def _run(x4: torch.Tensor, out4: torch.Tensor, weight: Optional[torch.Tensor], e
     os_ = _lib.strides2((out4.stride(0), out4.stride(1)))
     stream = torch.cuda.current_stream(x4.device).cuda_stream
     with torch.cuda.device(x4.device):
-        rc = _lib.lib().vx_rmsnorm_rope_fwd(
+        rc = _lib.lib().vx_rmsnorm_scale_rope_fwd(
             x4.data_ptr(), out4.data_ptr(),
             weight.data_ptr() if weight is not None else None, ctypes.c_float(eps), int(per_head),
-            cos_t.data_ptr() if cos_t is not None else None, sin_t.data_ptr() if sin_t is not None else None,
+            ctypes.c_float(post_scale), cos_t.data_ptr() if cos_t is not None else None, sin_t.data_ptr() if sin_t is not None else None,
             stride, B, S, H, D, xs, os_, ctypes.c_void_p(stream))
     _lib.raise_for(rc)
 
@@ -163,3 +167,89 @@ def qk_norm_rope(x: torch.Tensor, scale: Optional[torch.Tensor], freqs, num_head
     tables = _tables(freqs, S, D // 2, x.device) if freqs is not None else None
     _run(x4, out4, weight, float(eps), False, tables)
     return out4
+
+
+# ------------------------------------------------ neighbourhood-attention block
+def default_rope_dim_split(head_dim: int) -> Tuple[int, int, int]:
+    """(d_t, d_h, d_w) channels of head_dim given to the T, H and W rotations:
+    d_t = (head_dim // 4) rounded down to even, the rest halved, d_t lowered
+    by 2 when that half is odd (`diffusion_vae.py:96-103`)."""
+    d_t = (head_dim // 4) // 2 * 2
+    d_hw = (head_dim - d_t) // 2
+    if d_hw % 2:
+        d_t -= 2
+        d_hw = (head_dim - d_t) // 2
+    return d_t, d_hw, d_hw
+
+
+def create_abs_rope3d_freqs(t: int, h: int, w: int, head_dim: int,
+                            rope_split: Optional[Tuple[int, int, int]] = None, base: float = 10000.0,
+                            device=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-token tables of the absolute interleaved-pair RoPE of a (t, h, w)
+    grid: (cos, sin), each (1, t*h*w, 1, head_dim // 2) fp32. Pair j < d_t/2
+    turns by t_pos * inv_t[j], the next d_h/2 pairs by h_pos * inv_h, the last
+    d_w/2 by w_pos * inv_w, with inv = 1 / base^(arange(0, d, 2) / d) computed
+    in float64 and stored as fp32 and the angles formed in fp32
+    (`diffusion_vae.py:106-149,265-273`)."""
+    d_t, d_h, d_w = rope_split or default_rope_dim_split(head_dim)
+    if d_t + d_h + d_w != head_dim or d_t % 2 or d_h % 2 or d_w % 2:
+        raise ValueError(f"rope split {(d_t, d_h, d_w)} must be even and sum to head_dim {head_dim}")
+
+    def axis(n, d):
+        inv = 1.0 / torch.pow(torch.tensor(float(base), dtype=torch.float64),
+                              torch.arange(0, d, 2, dtype=torch.float64) / d)
+        ang = torch.arange(n, dtype=torch.float32, device=device)[:, None] * inv.to(torch.float32).to(device)[None, :]
+        return torch.cos(ang), torch.sin(ang)
+
+    ct, st = axis(t, d_t)
+    ch, sh = axis(h, d_h)
+    cw, sw = axis(w, d_w)
+
+    def grid(ft, fh, fw):
+        gt = ft[:, None, None, :].expand(t, h, w, d_t // 2)
+        gh = fh[None, :, None, :].expand(t, h, w, d_h // 2)
+        gw = fw[None, None, :, :].expand(t, h, w, d_w // 2)
+        return torch.cat([gt, gh, gw], dim=-1).reshape(1, t * h * w, 1, head_dim // 2)
+
+    return grid(ct, ch, cw), grid(st, sh, sw)
+
+
+def _check_grid(x: torch.Tensor) -> None:
+    _check_x(x)
+    if x.dim() != 6:
+        raise ValueError("x must be (B, T, H, W, num_heads, head_dim)")
+
+
+def apply_abs_rope3d(x: torch.Tensor, freqs) -> torch.Tensor:
+    """`_apply_abs_rope` (`diffusion_vae.py:130-149`) of x (B, T, H, W, NH,
+    HD) with tables from create_abs_rope3d_freqs: fp32 rotation of each
+    head's (even, odd) pairs, cast back to bf16."""
+    _check_grid(x)
+    B, T, H, W, NH, HD = x.shape
+    x4 = x.contiguous().reshape(B, T * H * W, NH, HD)
+    out4 = torch.empty_like(x4)
+    _run(x4, out4, None, 0.0, False, _tables(freqs, T * H * W, HD // 2, x.device))
+    return out4.reshape(x.shape)
+
+
+def na3d_qk_norm_rope(x: torch.Tensor, scale: Optional[torch.Tensor], freqs, eps: float = 1e-6,
+                      post_scale: float = 1.0) -> torch.Tensor:
+    """The q/k preparation of the neighbourhood-attention block in one pass
+    (`diffusion_vae.py:263-273`): per-head RMSNorm with weight `scale`
+    (head_dim,) (skipped when None), times `post_scale` as a bf16 scalar (q:
+    head_dim ** -0.5; k: 1.0), then the absolute RoPE with `freqs` from
+    create_abs_rope3d_freqs (skipped when None). x is (B, T, H, W, NH, HD)
+    bf16; the result has the same shape."""
+    _check_grid(x)
+    B, T, H, W, NH, HD = x.shape
+    x4 = x.contiguous().reshape(B, T * H * W, NH, HD)
+    out4 = torch.empty_like(x4)
+    weight = None
+    if scale is not None:
+        w = torch.as_tensor(scale, device=x.device).to(torch.float32).reshape(-1)
+        if w.numel() != HD:
+            raise ValueError(f"scale has {w.numel()} entries, head_dim is {HD}")
+        weight = w.repeat(NH).contiguous()
+    tables = _tables(freqs, T * H * W, HD // 2, x.device) if freqs is not None else None
+    _run(x4, out4, weight, float(eps), True, tables, float(post_scale))
+    return out4.reshape(x.shape)
