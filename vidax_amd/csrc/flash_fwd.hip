@@ -47,8 +47,9 @@ struct FCfg {
   static constexpr int kKBuf = 3 * kTileBytes;          // three K tiles
   static constexpr int kSmemBytes = 6 * kTileBytes;     // 96 (48) KiB
   static constexpr int kMaskBuf = 6 * kTileBytes;       // then the mask ring
-  static constexpr int kKeysPerCopy = 1024 / kRowBytes; // rows per 1 KiB DMA copy
-  static constexpr int kChunks = kRowBytes / 16;        // 16-byte chunks per row
+  // In LDS a tile is D/64 half-planes of 64 keys x 128 bytes (d 0-63, then
+  // d 64-127): one 1 KiB DMA copy fills 8 keys of one half-plane.
+  static constexpr int kHalfBytes = kBN * 128;          // 8 KiB
   static constexpr int kLoadsPerWave = kTileBytes / (kWaves * 1024);  // copies per wave per tile
   static constexpr int kDB = D / 32;                    // 32-wide d blocks of O
   static constexpr int kDS = D / 16;                    // 16-deep d steps of QK^T
@@ -70,11 +71,19 @@ constexpr float kRescaleSlack = 8.0f;         // log2 units
 constexpr float kSumLimit = 256.0f;           // 2^kRescaleSlack
 constexpr float kNegBig = -1.0e30f;           // finite "no key seen yet" max
 
-// XOR swizzle of the 16-byte chunk index (low 3 bits) within an LDS row.
-// Eight consecutive rows map one chunk to eight distinct 16-byte bank groups
-// (the ds_read_b128 K reads), and rows 4i..4i+3 map a chunk pair to four
-// distinct pairs (the transpose reads of V).
-__device__ __forceinline__ int row_swizzle(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// XOR swizzle of the 16-byte chunk index (0-7) within the 128-byte half row
+// of key r: the bit reversal of (r >> 1) & 7. The LDS has 64 four-byte banks
+// (256 bytes per cycle) and two consecutive half rows cover them once, so
+//  - the K reads (ds_read_b128, 16 lanes = keys 16i..16i+15 per cycle, one
+//    chunk index) hit 16 distinct 16-byte bank groups: the 8 even and the 8
+//    odd keys each see all 8 swizzles;
+//  - the V transpose reads (ds_read_b64_tr_b16, 32 lanes = keys 4i..4i+3,
+//    four chunks each, per cycle) hit 16 distinct groups: keys 4i, 4i+2 (and
+//    4i+1, 4i+3) differ in bit 2 of the swizzle.
+// Keys r and r + 8 differ only in bit 0 of the swizzle.
+__device__ __forceinline__ int half_swizzle(int r) {
+  return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
+}
 
 typedef VX_LDS unsigned char lds_u8;
 
@@ -105,7 +114,7 @@ template <int MASK, int D>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_fwd_kernel(const FlashArgs a) {
   using C = FCfg<D>;
-  constexpr int kRowBytes = C::kRowBytes, kTileBytes = C::kTileBytes, kVBuf = C::kVBuf, kKBuf = C::kKBuf;
+  constexpr int kTileBytes = C::kTileBytes, kVBuf = C::kVBuf, kKBuf = C::kKBuf;
   constexpr int kSmemBytes = C::kSmemBytes, kMaskBuf = C::kMaskBuf, kLoadsPerWave = C::kLoadsPerWave;
   constexpr int kDB = C::kDB, kDS = C::kDS, kPV = C::kPV, kSlots = C::kSlots;
   constexpr bool MASKED = MASK != kMaskNone;
@@ -142,31 +151,35 @@ void flash_fwd_kernel(const FlashArgs a) {
     for (int ds = 0; ds < kDS; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
   }
 
-  // ---- per-lane LDS byte offsets inside one tile.
-  // K fragment (kb, ds): row kb*32 + col, chunk 2*ds + hf, swizzled by col%8.
-  const int ksw = row_swizzle(col);
+  // ---- per-lane LDS byte offsets inside one tile (half-plane 0; the
+  // fragments of d 64-127 add kHalfBytes).
+  // K fragment (kb, ds): key kb*32 + col, chunk 2*(ds%4) + hf of half ds/4.
+  const int ksw = half_swizzle(col);
   int koff[4];
 #pragma unroll
-  for (int d4 = 0; d4 < 4; ++d4) koff[d4] = col * kRowBytes + (((2 * d4 + hf) ^ ksw) * 16);
+  for (int d4 = 0; d4 < 4; ++d4) koff[d4] = col * 128 + (((2 * d4 + hf) ^ ksw) * 16);
   // V transpose read (kb, j, db, e): group g = lane/16 covers columns
-  // db*32 + (g%2)*16 + 0..15 of rows kb*32 + 16j + 8e + hf*4 + 0..3.
+  // db*32 + (g%2)*16 + 0..15 of keys kb*32 + 16j + 8e + hf*4 + 0..3.
   const int i16 = lane & 15;
   const int vr = i16 >> 2, vc = i16 & 3, dh = (lane >> 4) & 1;
-  const int vsw = 2 * vr + hf;  // row_swizzle of those rows
-  int voff[2];
+  // e = 0 offsets; key + 8 flips bit 0 of the swizzle, so the e = 1 offset
+  // is (voff ^ 16) + 8 * 128.
+  int voff[2];  // [db & 1]
 #pragma unroll
-  for (int db1 = 0; db1 < 2; ++db1)
-    voff[db1] = (hf * 4 + vr) * kRowBytes + (((4 * db1 + 2 * dh + (vc >> 1)) ^ vsw) * 16) + (vc & 1) * 8;
-  // staging: this lane's row within its group of kKeysPerCopy rows and its
-  // 16-byte column
-  const int srow = lane / C::kChunks;
-  const int scol = lane % C::kChunks;
+  for (int db1 = 0; db1 < 2; ++db1) {
+    const int key = hf * 4 + vr;
+    voff[db1] = key * 128 + (((4 * db1 + 2 * dh + (vc >> 1)) ^ half_swizzle(key)) * 16) + (vc & 1) * 8;
+  }
+  // staging: copy i of a tile fills half-plane i / 8, keys 8*(i%8) + 0..7;
+  // lane L takes key 8*(i%8) + L/8 and 16-byte column L%8
+  const int srow = lane >> 3;
+  const int scol = lane & 7;
 
   // ---- global -> LDS staging of one 64-key tile on the LDS DMA path
-  // (global_load_lds_dwordx4): each wave instruction fills kKeysPerCopy
-  // consecutive rows (1 KiB), lane L landing at byte 16*L, so lane L fetches
-  // the global chunk that the swizzle places there. kLoadsPerWave
-  // instructions per wave per tile.
+  // (global_load_lds_dwordx4): each wave instruction fills 8 consecutive
+  // half rows (1 KiB), lane L landing at byte 16*L, so lane L fetches the
+  // global chunk that the swizzle places there. kLoadsPerWave instructions
+  // per wave per tile.
   // Tiles that lie wholly below kv_end add a uniform tile offset to per-lane
   // row pointers computed once; the tail tile clamps its rows to kv_end - 1.
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
@@ -174,9 +187,11 @@ void flash_fwd_kernel(const FlashArgs a) {
   const bf16* vlane[kLoadsPerWave];
 #pragma unroll
   for (int p = 0; p < kLoadsPerWave; ++p) {
-    const int r = (wave * kLoadsPerWave + p) * C::kKeysPerCopy + srow;
-    klane[p] = kg + (int64_t)r * a.ks[1] + ((scol ^ row_swizzle(r)) * 8);
-    vlane[p] = vg + (int64_t)r * a.vs[1] + ((scol ^ row_swizzle(r)) * 8);
+    const int i = wave * kLoadsPerWave + p;
+    const int r = 8 * (i & 7) + srow;
+    const int col_el = (i >> 3) * 64 + ((scol ^ half_swizzle(r)) * 8);
+    klane[p] = kg + (int64_t)r * a.ks[1] + col_el;
+    vlane[p] = vg + (int64_t)r * a.vs[1] + col_el;
   }
   auto stage = [&](const bf16* base, const bf16* const (&lanep)[kLoadsPerWave], int64_t sstride, int t,
                    int buf_off) {
@@ -184,15 +199,15 @@ void flash_fwd_kernel(const FlashArgs a) {
       const int64_t off = (int64_t)(t * kBN) * sstride;
 #pragma unroll
       for (int p = 0; p < kLoadsPerWave; ++p)
-        lds_dma16(lanep[p] + off, lds_base + buf_off + (wave * kLoadsPerWave + p) * C::kKeysPerCopy * kRowBytes);
+        lds_dma16(lanep[p] + off, lds_base + buf_off + (wave * kLoadsPerWave + p) * 1024);
     } else {
 #pragma unroll
       for (int p = 0; p < kLoadsPerWave; ++p) {
-        const int r0 = (wave * kLoadsPerWave + p) * C::kKeysPerCopy;
-        const int r = r0 + srow;
+        const int i = wave * kLoadsPerWave + p;
+        const int r = 8 * (i & 7) + srow;
         const int key = min(t * kBN + r, kv_end - 1);
-        const bf16* src = base + (int64_t)key * sstride + ((scol ^ row_swizzle(r)) * 8);
-        lds_dma16(src, lds_base + buf_off + r0 * kRowBytes);
+        const bf16* src = base + (int64_t)key * sstride + (i >> 3) * 64 + ((scol ^ half_swizzle(r)) * 8);
+        lds_dma16(src, lds_base + buf_off + i * 1024);
       }
     }
   };
@@ -205,7 +220,7 @@ void flash_fwd_kernel(const FlashArgs a) {
     for (int ds = 0; ds < kDS; ++ds) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 kf = *(const VX_LDS bf16x8*)(kb0 + koff[ds & 3] + kb * 32 * kRowBytes + (ds >> 2) * 128);
+        const bf16x8 kf = *(const VX_LDS bf16x8*)(kb0 + koff[ds & 3] + kb * 32 * 128 + (ds >> 2) * C::kHalfBytes);
         S[kb] = mfma32x32x16(kf, qr[ds], S[kb]);
       }
     }
@@ -218,9 +233,10 @@ void flash_fwd_kernel(const FlashArgs a) {
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int db = 0; db < kDB; ++db) {
-          const lds_u8* p = vb + voff[db & 1] + (kb * 32 + 16 * j) * kRowBytes + (db >> 1) * 128;
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p);
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + 8 * kRowBytes));
+          const lds_u8* p = vb + (kb * 32 + 16 * j) * 128 + (db >> 1) * C::kHalfBytes;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + voff[db & 1]));
+          const s16x4 hi =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + 8 * 128 + (voff[db & 1] ^ 16)));
           const bf16x8 vf = concat(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi));
           O[db] = mfma32x32x16(vf, P[kb][j], O[db]);
         }
@@ -382,13 +398,14 @@ void flash_fwd_kernel(const FlashArgs a) {
         auto frag = [&](int s) -> bf16x8 {
           if (s < kPV) {
             const int db = s % kDB, j = (s / kDB) & 1, kb = s / (2 * kDB);
-            const lds_u8* p = vb0 + voff[db & 1] + (kb * 32 + 16 * j) * kRowBytes + (db >> 1) * 128;
-            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p);
-            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + 8 * kRowBytes));
+            const lds_u8* p = vb0 + (kb * 32 + 16 * j) * 128 + (db >> 1) * C::kHalfBytes;
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + voff[db & 1]));
+            const s16x4 hi =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + 8 * 128 + (voff[db & 1] ^ 16)));
             return concat(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi));
           }
           const int ds = (s - kPV) >> 1, kb = (s - kPV) & 1;
-          return *(const VX_LDS bf16x8*)(kb0 + koff[ds & 3] + kb * 32 * kRowBytes + (ds >> 2) * 128);
+          return *(const VX_LDS bf16x8*)(kb0 + koff[ds & 3] + kb * 32 * 128 + (ds >> 2) * C::kHalfBytes);
         };
         const float mneg = -m_run;
         const bf16x2 one2 = {(bf16)1.0f, (bf16)1.0f};
