@@ -32,6 +32,16 @@ constexpr float kNegBig = -1.0e30f;
 
 __device__ __forceinline__ int row_swizzle(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
+// XOR swizzle of the 16-byte chunk index (0-7) within the 128-byte half row
+// of key slot r (the bit reversal of (r >> 1) & 7), for the pipelined kernel's
+// half-plane layout on the 64-bank LDS: any 16 consecutive slots (a K read of
+// 16 lanes) and any 4 consecutive slots x 4 chunks (a V transpose read of 32
+// lanes) fall on distinct 16-byte bank groups. Slots r and r + 8 differ only
+// in bit 0 of the swizzle.
+__device__ __forceinline__ int half_swizzle(int r) {
+  return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
+}
+
 __device__ __forceinline__ int window_start(int i, int len, int k) {
   return min(max(i - k / 2, 0), len - k);
 }
@@ -263,16 +273,18 @@ struct PipeCfg {
   static constexpr int kWaves = 4;
   static constexpr int kThreads = kWaves * 64;
   static constexpr int kBrickY = 4, kBrickX = 32;
-  static constexpr int kRB = D * 2;                      // bytes of one key row
-  static constexpr int kChunks = kRB / 16;               // 16-byte chunks per key row (16 or 8)
-  static constexpr int kKeysPerCopy = 1024 / kRB;        // key rows per 1 KiB DMA copy (4 or 8)
+  static constexpr int kRB = D * 2;                      // bytes of one key
   static constexpr int kRows = SEG == 16 ? 2 : 1;        // key rows per step
   static constexpr int kNS = SEG == 16 ? 40 : 64;        // key slots per LDS row (>= 24 + SEG)
+  // An LDS key row is D/64 half-planes of kNS slots x 128 bytes (d 0-63,
+  // then d 64-127); one 1 KiB DMA copy fills 8 slots of one half-plane.
+  static constexpr int kHalfL = kNS * 128;               // one half-plane of a row
   static constexpr int kRowL = kNS * kRB;                // one LDS key row
+  static constexpr int kKeysPerCopy = 8;
   static constexpr int kSlot = kRows * kRowL;            // one ring slot: one tensor, one step
   static constexpr int kK = 0, kV = 2 * kSlot;           // K slots 0,1 then V slots 0,1
   static constexpr int kSmem = 4 * kSlot;
-  static constexpr int kCopies = kRows * kNS / kKeysPerCopy;  // DMA copies per tensor per step
+  static constexpr int kCopies = kRows * kRowL / 1024;   // DMA copies per tensor per step
   // copies past kCopies repeat the last one (same bytes, same place), so every
   // wave issues the same number of copies
   static constexpr int kCopiesPerWave = (kCopies + kWaves - 1) / kWaves;
@@ -280,7 +292,7 @@ struct PipeCfg {
   static constexpr int kPV = 2 * (D / 32);               // MFMAs of PV per chunk
   static constexpr int kSlots = kQK + kPV;
   static constexpr int kScoresPerSlot = 16 / kSlots;     // softmax work per slot (1 or 2)
-  static_assert(kNS % kKeysPerCopy == 0, "whole copies per row");
+  static_assert(kNS % kKeysPerCopy == 0 && kHalfL % 256 == 0, "whole copies per row, bank-aligned planes");
 };
 
 __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_row) {
@@ -305,7 +317,6 @@ template <int SEG, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   using C = PipeCfg<SEG, D>;
-  constexpr int kRowBytes = C::kRB;
   __shared__ __attribute__((aligned(16))) unsigned char smem[C::kSmem];
   VX_LDS unsigned char* const lds = (VX_LDS unsigned char*)smem;
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
@@ -380,23 +391,26 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
     for (int ds = 0; ds < C::kQK; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
   }
 
-  // ---- DMA of one step of one tensor: copy i covers LDS row i / (kNS/n) of
-  // the slot and key slots n*(i % (kNS/n)) + 0..n-1 (n = kKeysPerCopy); wave
-  // w issues copies w, w + 4, ... The lane-dependent part of each copy's
-  // source (x position, swizzled 16-byte chunk) is fixed for the workgroup;
-  // the row tokens change per step and are scalar.
-  constexpr int kGroups = C::kNS / C::kKeysPerCopy;  // copies per LDS row
-  const int srow = lane / C::kChunks, scol = lane % C::kChunks;
+  // ---- DMA of one step of one tensor: copy i covers LDS row i / G of the
+  // slot (G = kRowL / 1 KiB copies per row), half-plane (i % G) / (kNS/8)
+  // and key slots 8*((i % G) % (kNS/8)) + 0..7; wave w issues copies w,
+  // w + 4, ... The lane-dependent part of each copy's source (x position,
+  // half, swizzled 16-byte chunk) is fixed for the workgroup; the row tokens
+  // change per step and are scalar.
+  constexpr int kGroups = C::kRowL / 1024;           // copies per LDS row
+  constexpr int kGroupsPerHalf = C::kNS / C::kKeysPerCopy;
+  const int srow = lane >> 3, scol = lane & 7;
   int64_t dma_off[C::kCopiesPerWave];
   int dma_dst[C::kCopiesPerWave], dma_row[C::kCopiesPerWave];
 #pragma unroll
   for (int p = 0; p < C::kCopiesPerWave; ++p) {
     const int i = min(wave + C::kWaves * p, C::kCopies - 1);
     const int g = i % kGroups;
-    const int pos = C::kKeysPerCopy * g + srow;
+    const int half = g / kGroupsPerHalf;
+    const int pos = C::kKeysPerCopy * (g % kGroupsPerHalf) + srow;
     dma_row[p] = i / kGroups;
-    dma_dst[p] = dma_row[p] * C::kRowL + C::kKeysPerCopy * g * kRowBytes;
-    dma_off[p] = (int64_t)min(X_lo + pos, W - 1) * tok_stride + ((scol ^ row_swizzle(pos)) * 8);
+    dma_dst[p] = dma_row[p] * C::kRowL + g * 1024;
+    dma_off[p] = (int64_t)min(X_lo + pos, W - 1) * tok_stride + half * 64 + ((scol ^ half_swizzle(pos)) * 8);
   }
   // Box rows are walked with cursors (row index, its y in the box, its token
   // offset) that advance one row at a time and stop at the last row, so no
@@ -429,17 +443,18 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
       lds_dma16(base + (dma_row[p] ? rt1 : rt0) + dma_off[p], lds_base + slot_off + dma_dst[p]);
   };
 
-  // ---- per-lane LDS offsets. K fragment: key col of the chunk (SEG = 16:
-  // keys 0-15 from the step's first row, 16-31 from its second).
+  // ---- per-lane LDS offsets (half-plane 0; d 64-127 add kHalfL). K
+  // fragment: key col of the chunk (SEG = 16: keys 0-15 from the step's first
+  // row, 16-31 from its second).
   int kbase, ksw;
   if (SEG == 16) {
     const int pos = ox + (col & 15);
-    kbase = (col >> 4) * C::kRowL + pos * kRowBytes;
-    ksw = row_swizzle(pos);
+    kbase = (col >> 4) * C::kRowL + pos * 128;
+    ksw = half_swizzle(pos);
   } else {
     const int pos = ox + col;
-    kbase = pos * kRowBytes;
-    ksw = row_swizzle(pos);
+    kbase = pos * 128;
+    ksw = half_swizzle(pos);
   }
   int koff[4];
 #pragma unroll
@@ -451,21 +466,21 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     const int pos = ox + 8 * e + 4 * hf + vr;
-    const int sw = row_swizzle(pos);
+    const int sw = half_swizzle(pos);
 #pragma unroll
     for (int db1 = 0; db1 < 2; ++db1)
-      voff[e][db1] = pos * kRowBytes + (((4 * db1 + 2 * dh + (vc >> 1)) ^ sw) * 16) + (vc & 1) * 8;
+      voff[e][db1] = pos * 128 + (((4 * db1 + 2 * dh + (vc >> 1)) ^ sw) * 16) + (vc & 1) * 8;
   }
   auto vfrag = [&](const VX_LDS unsigned char* vb, int j, int db) -> bf16x8 {
-    const int jo = SEG == 16 ? j * C::kRowL : j * 16 * kRowBytes;
-    const VX_LDS unsigned char* p0 = vb + jo + voff[0][db & 1] + (db >> 1) * 128;
-    const VX_LDS unsigned char* p1 = vb + jo + voff[1][db & 1] + (db >> 1) * 128;
+    const int jo = SEG == 16 ? j * C::kRowL : j * 16 * 128;
+    const VX_LDS unsigned char* p0 = vb + jo + voff[0][db & 1] + (db >> 1) * C::kHalfL;
+    const VX_LDS unsigned char* p1 = vb + jo + voff[1][db & 1] + (db >> 1) * C::kHalfL;
     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p0);
     const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)p1);
     return concat(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi));
   };
   auto kfrag = [&](const VX_LDS unsigned char* kb, int ds) -> bf16x8 {
-    return *(const VX_LDS bf16x8*)(kb + koff[ds & 3] + (ds >> 2) * 128);
+    return *(const VX_LDS bf16x8*)(kb + koff[ds & 3] + (ds >> 2) * C::kHalfL);
   };
   constexpr int kDB = D / 32;  // 32-wide d blocks of O
 
