@@ -75,6 +75,34 @@ def test_flash_small(gpu, B, Sq, Sk, H, seed, mask):
     _check(out, ref, "oracle")
 
 
+ROW_SHIFTS = [-1000.0, -120.0, 200.0, 1000.0]
+
+
+@pytest.mark.parametrize("shift", ROW_SHIFTS)
+@pytest.mark.parametrize("masked", [False, True])
+def test_flash_row_offsets(gpu, shift, masked):
+    """A constant added to every score of a query row leaves its softmax
+    unchanged. Key dim 0 is all ones and the query's dim 0 is `shift` (every
+    other query row 0), scale 1: rows whose scores all lie far below 2^-100
+    or far above 2^8 (log2 units) next to ordinary rows in the same wave
+    must still match the oracle, which subtracts each row's max."""
+    from vidax_amd import flash_attention
+    _say(f"flash row offsets shift={shift} masked={masked}")
+    B, Sq, Sk, H, D = 2, 96, 300, 2, 128
+    rng = np.random.default_rng(70)
+    q = O.bf16_round((0.3 * rng.standard_normal((B, Sq, H, D))).astype(np.float32))
+    k = O.bf16_round((0.3 * rng.standard_normal((B, Sk, H, D))).astype(np.float32))
+    v = O.bf16_round(rng.standard_normal((B, Sk, H, D)).astype(np.float32))
+    k[..., 0] = 1.0
+    q[:, ::2, :, 0] = shift
+    q[:, 1::2, :, 0] = 0.0
+    kv_len = np.array([Sk, 170], np.int32) if masked else None
+    out = flash_attention(_t(q, gpu), _t(k, gpu), _t(v, gpu), scale=1.0,
+                          kv_len=torch.from_numpy(kv_len).to(gpu) if masked else None)
+    torch.cuda.synchronize()
+    _check(out, O.attention(q, k, v, scale=1.0, kv_len=kv_len), "oracle")
+
+
 def test_flash_sk1_returns_v(gpu):
     """Sk = 1: every query attends one key with weight 1, so out = v."""
     from vidax_amd import flash_attention

@@ -83,6 +83,28 @@ def test_na3d_head_dim_64(gpu, shape, ks, seed):
     _check(out.float().cpu().numpy(), O.na3d(q, k, v, ks), "oracle")
 
 
+@pytest.mark.parametrize("shift", [-1000.0, -120.0, 200.0, 1000.0])
+@pytest.mark.parametrize("D", [128, 64])
+def test_na3d_row_offsets(gpu, shift, D):
+    """A constant added to every score of a query leaves its softmax
+    unchanged: key dim 0 all ones, the query's dim 0 = `shift` on every other
+    x position (0 elsewhere), so queries far below 2^-100 or far above 2^8
+    (log2 units) sit next to ordinary ones in the same wave."""
+    from vidax_amd import neighborhood_attention_3d
+    _say(f"na3d row offsets shift={shift} D={D}")
+    B, T, H, W, NH = 1, 3, 9, 20, 2
+    rng = np.random.default_rng(71)
+    q = O.bf16_round((0.3 * rng.standard_normal((B, T, H, W, NH, D))).astype(np.float32))
+    k = O.bf16_round((0.3 * rng.standard_normal((B, T, H, W, NH, D))).astype(np.float32))
+    v = O.bf16_round(rng.standard_normal((B, T, H, W, NH, D)).astype(np.float32))
+    k[..., 0] = 1.0
+    q[:, :, :, ::2, :, 0] = shift
+    q[:, :, :, 1::2, :, 0] = 0.0
+    out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), (3, 7, 7))
+    torch.cuda.synchronize()
+    _check(out.float().cpu().numpy(), O.na3d(q, k, v, (3, 7, 7)), "oracle")
+
+
 def test_na3d_window_one_is_identity(gpu):
     from vidax_amd import neighborhood_attention_3d
     _say("na3d window (1,1,1) identity")
