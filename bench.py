@@ -211,6 +211,7 @@ def main(argv=None):
     import torch
     import vidax_amd
     from vidax_amd import _lib
+    from vidax_amd.attention import flash_kernel_name
 
     _lib.lib()
     dev = torch.device("cuda:0")
@@ -223,7 +224,7 @@ def main(argv=None):
         def step():
             vidax_amd.flash_attention(q, k, v, out=out, **kw)
         mask_kind = (1 if "key_valid" in kw else 0) | (2 if "key_bias" in kw else 0)
-        kernel_name = f"flash_fwd_kernel<{mask_kind}, 128>"
+        kernel_name = flash_kernel_name(p["B"], p["Sq"], p["Sk"], p["H"], 128, mask_kind)
     elif kind == "prologue":
         from vidax_amd.prologue import create_rope3d_freqs, qk_norm_rope
         g = torch.Generator(device=dev)

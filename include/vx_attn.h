@@ -64,8 +64,8 @@ const char* vx_last_error(void);
  * Strides (element units, {batch, seq, head}) may be NULL for a contiguous
  * (B, S, H, D) tensor; the head dim must be contiguous. q/k/v/out must be
  * 16-byte aligned and every stride a multiple of 8 elements.
- * Supported: head_dim == 128, scale > 0 and finite, 1 <= B, H <= 65535 and
- * 1 <= Sq, Sk < 2^31.
+ * Supported: head_dim 64 or 128, scale > 0 and finite, 1 <= B, H <= 65535,
+ * 1 <= Sq, Sk < 2^31, k and v sequence strides <= 2^24 elements.
  * `stream` is a hipStream_t (NULL = the default stream).
  */
 int32_t vx_flash_attn_fwd(const void* q, const void* k, const void* v, void* out,

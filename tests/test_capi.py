@@ -66,6 +66,8 @@ def test_flash_check_accepts_valid_arguments():
     (dict(scale=-1.0), _lib.VX_ERR_INVALID_ARGUMENT, "scale"),
     (dict(qs=(0, 4 * 128, 129)), _lib.VX_ERR_INVALID_ARGUMENT, "multiple of 8"),
     (dict(ks=(0, -512, 128)), _lib.VX_ERR_INVALID_ARGUMENT, "negative"),
+    (dict(ks=(0, (1 << 24) + 8, 128)), _lib.VX_ERR_UNSUPPORTED, "2^24"),
+    (dict(vs=(0, 1 << 25, 128)), _lib.VX_ERR_UNSUPPORTED, "2^24"),
     (dict(key_valid=A, stride=200), _lib.VX_ERR_INVALID_ARGUMENT, "key_mask_stride"),
     (dict(key_valid=A, stride=258), _lib.VX_ERR_INVALID_ARGUMENT, "key_mask_stride"),
     (dict(key_valid=A + 2, stride=256), _lib.VX_ERR_INVALID_ARGUMENT, "4-byte"),
@@ -240,3 +242,15 @@ def test_flash_bias_check():
     assert _bias_check(strides=None) == _lib.VX_ERR_INVALID_ARGUMENT
     assert _bias_check(D=64) == _lib.VX_OK
     assert _bias_check(D=96) == _lib.VX_ERR_UNSUPPORTED
+
+
+def test_flash_kernel_name_follows_the_launch_rule():
+    """The profiling name mirrors the launcher: 128-query workgroups for key
+    sequences up to 1024 or fewer than 768 256-query tiles, else 256-query."""
+    from vidax_amd.attention import flash_kernel_name
+    assert flash_kernel_name(1, 32760, 32760, 40) == "flash_fwd_kernel<0, 128, 8>"
+    assert flash_kernel_name(1, 119056, 119056, 24, 128, 1) == "flash_fwd_kernel<1, 128, 8>"
+    assert flash_kernel_name(1, 7800, 7800, 12) == "flash_fwd_kernel<0, 128, 4>"      # 372 tiles
+    assert flash_kernel_name(2, 32760, 512, 40) == "flash_fwd_kernel<0, 128, 4>"      # short keys
+    assert flash_kernel_name(1, 200, 200, 4, 64, 4) == "flash_fwd_kernel<4, 64, 4>"
+    assert flash_kernel_name(3, 65536, 1025, 1) == "flash_fwd_kernel<0, 128, 8>"      # 768 tiles

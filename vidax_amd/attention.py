@@ -20,6 +20,7 @@ from . import _lib
 
 __all__ = [
     "flash_attention",
+    "flash_kernel_name",
     "local_attention",
     "dot_product_attention",
     "masked_self_attention",
@@ -166,6 +167,17 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
             ctypes.c_float(scale), ctypes.c_void_p(stream))
     _lib.raise_for(rc)
     return out
+
+
+def flash_kernel_name(batch: int, seq_q: int, seq_k: int, num_heads: int, head_dim: int = 128,
+                      mask_kind: int = 0) -> str:
+    """Name of the kernel the library launches (profiling aid): 128-query
+    workgroups (4 waves) for key sequences up to 1024 or grids of fewer than
+    768 256-query tiles, 256-query workgroups (8 waves) otherwise. mask_kind:
+    1 key validity, 2 key bias, 4 full bias (bits)."""
+    blocks256 = -(-int(seq_q) // 256) * int(num_heads) * int(batch)
+    waves = 4 if int(seq_k) <= 1024 or blocks256 < 768 else 8
+    return f"flash_fwd_kernel<{int(mask_kind)}, {int(head_dim)}, {waves}>"
 
 
 def _single_device(mesh) -> None:

@@ -34,23 +34,29 @@ namespace vx {
 namespace {
 
 constexpr int kBN = 64;                       // keys per tile
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
-constexpr int kQueriesPerBlock = kWaves * 32;
 
-// Per head dim (128 or 64): LDS rows, tiles, buffers and DMA copies.
-template <int D>
+// Per head dim (128 or 64) and workgroup size: LDS rows, tiles, buffers and
+// DMA copies. 8 waves (256 queries) keep three K and three V tiles (one
+// workgroup per CU, copies issued two iterations ahead); 4 waves (128
+// queries) keep two of each, so that two workgroups share a CU and hide each
+// other's start (q load, pipeline fill) and end, which dominate short key
+// sequences and small grids.
+template <int D, int WAVES>
 struct FCfg {
+  static constexpr int kWaves = WAVES;
+  static constexpr int kThreads = WAVES * 64;
+  static constexpr int kQueriesPerBlock = WAVES * 32;
+  static constexpr int kNB = WAVES == 8 ? 3 : 2;        // K (and V) tiles in LDS
   static constexpr int kRowBytes = D * 2;               // one bf16 key row
   static constexpr int kTileBytes = kBN * kRowBytes;    // 16 (8) KiB
-  static constexpr int kVBuf = 0;                       // three V tiles
-  static constexpr int kKBuf = 3 * kTileBytes;          // three K tiles
-  static constexpr int kSmemBytes = 6 * kTileBytes;     // 96 (48) KiB
-  static constexpr int kMaskBuf = 6 * kTileBytes;       // then the mask ring
+  static constexpr int kVBuf = 0;                       // kNB V tiles
+  static constexpr int kKBuf = kNB * kTileBytes;        // kNB K tiles
+  static constexpr int kSmemBytes = 2 * kNB * kTileBytes;
+  static constexpr int kMaskBuf = kSmemBytes;           // then the mask ring
   // In LDS a tile is D/64 half-planes of 64 keys x 128 bytes (d 0-63, then
   // d 64-127): one 1 KiB DMA copy fills 8 keys of one half-plane.
   static constexpr int kHalfBytes = kBN * 128;          // 8 KiB
-  static constexpr int kLoadsPerWave = kTileBytes / (kWaves * 1024);  // copies per wave per tile
+  static constexpr int kLoadsPerWave = kTileBytes / (WAVES * 1024);  // copies per wave per tile
   static constexpr int kDB = D / 32;                    // 32-wide d blocks of O
   static constexpr int kDS = D / 16;                    // 16-deep d steps of QK^T
   static constexpr int kPV = 2 * 2 * kDB;               // MFMAs of PV per tile
@@ -110,10 +116,11 @@ __device__ __forceinline__ void wait_vmem() {
 // NaN test on the bit pattern (stays exact when the compiler may assume no NaNs).
 __device__ __forceinline__ bool is_nan_bits(float x) { return (__float_as_uint(x) & 0x7fffffffu) > 0x7f800000u; }
 
-template <int MASK, int D>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int MASK, int D, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_fwd_kernel(const FlashArgs a) {
-  using C = FCfg<D>;
+  using C = FCfg<D, WAVES>;
+  constexpr int kWaves = C::kWaves, kThreads = C::kThreads, kNB = C::kNB;
   constexpr int kTileBytes = C::kTileBytes, kVBuf = C::kVBuf, kKBuf = C::kKBuf;
   constexpr int kSmemBytes = C::kSmemBytes, kMaskBuf = C::kMaskBuf, kLoadsPerWave = C::kLoadsPerWave;
   constexpr int kDB = C::kDB, kDS = C::kDS, kPV = C::kPV, kSlots = C::kSlots;
@@ -183,23 +190,38 @@ void flash_fwd_kernel(const FlashArgs a) {
   // Tiles that lie wholly below kv_end add a uniform tile offset to per-lane
   // row pointers computed once; the tail tile clamps its rows to kv_end - 1.
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
-  const bf16* klane[kLoadsPerWave];
-  const bf16* vlane[kLoadsPerWave];
+  // per-lane sources of the copies within tile 0: pointers with 8 waves
+  // (two copies per wave per tile), 32-bit element offsets from k / v with 4
+  // waves (four copies; a tile spans 63 rows of the key stride, well inside
+  // 32 bits) to save registers
+  using LaneSrc = std::conditional_t<WAVES == 8, const bf16*, int>;
+  LaneSrc klane[kLoadsPerWave];
+  LaneSrc vlane[kLoadsPerWave];
 #pragma unroll
   for (int p = 0; p < kLoadsPerWave; ++p) {
     const int i = wave * kLoadsPerWave + p;
     const int r = 8 * (i & 7) + srow;
     const int col_el = (i >> 3) * 64 + ((scol ^ half_swizzle(r)) * 8);
-    klane[p] = kg + (int64_t)r * a.ks[1] + col_el;
-    vlane[p] = vg + (int64_t)r * a.vs[1] + col_el;
+    if constexpr (WAVES == 8) {
+      klane[p] = kg + (int64_t)r * a.ks[1] + col_el;
+      vlane[p] = vg + (int64_t)r * a.vs[1] + col_el;
+    } else {
+      klane[p] = r * (int)a.ks[1] + col_el;
+      vlane[p] = r * (int)a.vs[1] + col_el;
+    }
   }
-  auto stage = [&](const bf16* base, const bf16* const (&lanep)[kLoadsPerWave], int64_t sstride, int t,
-                   int buf_off) {
+  auto stage = [&](const bf16* base, const LaneSrc (&lanep)[kLoadsPerWave], int64_t sstride, int t, int buf_off) {
     if ((t + 1) * kBN <= kv_end) {
       const int64_t off = (int64_t)(t * kBN) * sstride;
 #pragma unroll
-      for (int p = 0; p < kLoadsPerWave; ++p)
-        lds_dma16(lanep[p] + off, lds_base + buf_off + (wave * kLoadsPerWave + p) * 1024);
+      for (int p = 0; p < kLoadsPerWave; ++p) {
+        const bf16* src;
+        if constexpr (WAVES == 8)
+          src = lanep[p] + off;
+        else
+          src = base + off + lanep[p];
+        lds_dma16(src, lds_base + buf_off + (wave * kLoadsPerWave + p) * 1024);
+      }
     } else {
 #pragma unroll
       for (int p = 0; p < kLoadsPerWave; ++p) {
@@ -282,33 +304,43 @@ void flash_fwd_kernel(const FlashArgs a) {
       if (lane < 16) lds_dma16(brow + j * kBN + lane * 4, slot + 64);
     }
   };
-  // This wave's DMA instructions of one iteration: the previous iteration's
-  // may still be in flight at the top of the next one.
+  // At the top of an iteration: with three tiles per ring the previous
+  // iteration's DMA instructions may still be in flight; with two, the tiles
+  // read next were issued by the previous iteration, so all have to land.
   auto wait_prev = [&]() {
-    if (MASKED && wave == 0)
+    if (kNB == 2)
+      wait_vmem<0>();
+    else if (MASKED && wave == 0)
       wait_vmem<2 * kLoadsPerWave + kMaskCopies>();
     else
       wait_vmem<2 * kLoadsPerWave>();
   };
 
   if (n_tiles > 0) {
-    // Tile j of K lives in K buffer j % 3 and tile j of V in V buffer j % 3;
-    // V buffer 2 stands in for "V_{-1}" (zeros, paired with P = 0 in
-    // iteration 0). Iteration t issues K_{t+3} and V_{t+1}, two iterations
-    // before they are read, so their latency is hidden.
-    // masks of tiles 0-2 first: they are older than every copy the first
-    // iterations wait for
+    // Tile j of K lives in K buffer j % kNB and tile j of V in V buffer
+    // j % kNB; V buffer kNB-1 stands in for "V_{-1}" (zeros, paired with P = 0
+    // in iteration 0). Iteration t issues K_{t+kNB} and V_{t+kNB-2}, into the
+    // buffers that the previous iteration finished reading.
+    // masks of the first tiles first: they are older than every copy the
+    // first iterations wait for
     stage_mask(0);
     stage_mask(min(1, n_tiles - 1));
-    stage_mask(min(2, n_tiles - 1));
+    if (kNB == 3) stage_mask(min(2, n_tiles - 1));
     stage(kg, klane, a.ks[1], 0, kKBuf);
     stage(kg, klane, a.ks[1], min(1, n_tiles - 1), kKBuf + kTileBytes);
-    stage(kg, klane, a.ks[1], min(2, n_tiles - 1), kKBuf + 2 * kTileBytes);
-    stage(vg, vlane, a.vs[1], 0, kVBuf);
+    if (kNB == 3) {
+      stage(kg, klane, a.ks[1], min(2, n_tiles - 1), kKBuf + 2 * kTileBytes);
+      stage(vg, vlane, a.vs[1], 0, kVBuf);
+    }
 #pragma unroll
     for (int p = 0; p < kTileBytes / (kThreads * 16); ++p)
-      *(VX_LDS u32x4*)(lds + kVBuf + 2 * kTileBytes + (p * kThreads + threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
-    wait_vmem<2 * kLoadsPerWave>();  // K_0 and K_1 have landed
+      *(VX_LDS u32x4*)(lds + kVBuf + (kNB - 1) * kTileBytes + (p * kThreads + threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
+    // K_0 (and K_1) have landed: the copies issued after them may still be
+    // in flight
+    if (kNB == 3)
+      wait_vmem<2 * kLoadsPerWave>();
+    else
+      wait_vmem<kLoadsPerWave>();
     __syncthreads();
     f32x16 S[2];
     qk(kKBuf, S);
@@ -318,23 +350,22 @@ void flash_fwd_kernel(const FlashArgs a) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) Pp[kb][j] = bf16x8{};
 
-    int kb_cur = 1;   // K buffer holding K_{t+1}  (= (t+1) % 3)
-    int vb_prev = 2;  // V buffer holding V_{t-1}  (= (t+2) % 3)
+    int kb_cur = 1;         // K buffer holding K_{t+1}  (= (t+1) % kNB)
+    int vb_prev = kNB - 1;  // V buffer holding V_{t-1}  (= (t+kNB-1) % kNB)
     // One key tile: consumes S (scores of tile t) and Pp (probabilities of
     // tile t-1), produces Sn (scores of tile t+1) and P (probabilities of
     // tile t). The loop below calls it twice per trip with the two register
     // sets swapped, so no copies are needed between tiles.
     auto step = [&](const int t, f32x16 (&S)[2], f32x16 (&Sn)[2], const bf16x8 (&Pp)[2][2],
                     bf16x8 (&P)[2][2]) {
-      // Tiles issued two iterations ago (K_{t+1}, V_{t-1}) have landed once
-      // only the previous iteration's 2 * kLoadsPerWave DMA instructions may
-      // still be outstanding; the barrier then publishes them, and it also
-      // frees K buffer t % 3 (K_t, read by QK(t) last iteration) and V buffer
-      // (t+1) % 3 (V_{t-2}) for this iteration's prefetch.
+      // K_{t+1} and V_{t-1} have landed once wait_prev returns; the barrier
+      // then publishes them, and it also frees K buffer t % kNB (K_t, read by
+      // QK(t) last iteration) and V buffer (t+kNB-2) % kNB (V_{t-2}) for this
+      // iteration's copies.
       wait_prev();
       __syncthreads();
-      const int kb_next = kb_cur == 0 ? 2 : kb_cur - 1;  // t % 3
-      const int vb_next = vb_prev == 2 ? 1 : (vb_prev == 1 ? 0 : 2);  // (t+1) % 3
+      const int kb_next = kb_cur == 0 ? kNB - 1 : kb_cur - 1;                    // t % kNB
+      const int vb_next = kNB == 2 ? kb_next : (vb_prev == 2 ? 1 : (vb_prev == 1 ? 0 : 2));  // (t+kNB-2) % kNB
 
       // ---- key masks. Tiles that hold a masked key (the tail tile, a
       // key_valid hole, any key_bias) take the scores to log2 units here,
@@ -357,9 +388,9 @@ void flash_fwd_kernel(const FlashArgs a) {
         slow = slow || __builtin_amdgcn_ballot_w64(hole) != 0;
       }
       if (MASK & (kMaskBias | kMaskFull)) slow = true;
-      stage(kg, klane, a.ks[1], min(t + 3, n_tiles - 1), kKBuf + kb_next * kTileBytes);
-      stage_mask(min(t + 3, n_tiles - 1));
-      stage(vg, vlane, a.vs[1], min(t + 1, n_tiles - 1), kVBuf + vb_next * kTileBytes);
+      stage(kg, klane, a.ks[1], min(t + kNB, n_tiles - 1), kKBuf + kb_next * kTileBytes);
+      stage_mask(min(t + kNB, n_tiles - 1));
+      stage(vg, vlane, a.vs[1], min(t + kNB - 2, n_tiles - 1), kVBuf + vb_next * kTileBytes);
       float cc = c;
       if (slow) {
         cc = 1.0f;
@@ -463,8 +494,8 @@ void flash_fwd_kernel(const FlashArgs a) {
         l_tile = probs(S, cc, m_run, P);
       }
       l_run += l_tile;
-      kb_cur = kb_cur == 2 ? 0 : kb_cur + 1;
-      vb_prev = vb_prev == 2 ? 0 : vb_prev + 1;
+      kb_cur = kb_cur == kNB - 1 ? 0 : kb_cur + 1;
+      vb_prev = vb_prev == kNB - 1 ? 0 : vb_prev + 1;
     };
 
     f32x16 S2[2];
@@ -505,14 +536,24 @@ void flash_fwd_kernel(const FlashArgs a) {
   }
 }
 
+template <int MASK, int WAVES>
+int launch_waves(const FlashArgs& a, hipStream_t stream) {
+  dim3 grid((a.Sq + WAVES * 32 - 1) / (WAVES * 32), a.H, a.B);
+  if (a.D == 64)
+    hipLaunchKernelGGL((flash_fwd_kernel<MASK, 64, WAVES>), grid, dim3(WAVES * 64), 0, stream, a);
+  else
+    hipLaunchKernelGGL((flash_fwd_kernel<MASK, 128, WAVES>), grid, dim3(WAVES * 64), 0, stream, a);
+  return (int)hipGetLastError();
+}
+
+// Short key sequences (few tiles per query tile) and grids that give most
+// CUs fewer than two 256-query workgroups run on 128-query workgroups, two
+// per CU; long sequences on 256-query workgroups.
 template <int MASK>
 int launch(const FlashArgs& a, hipStream_t stream) {
-  dim3 grid((a.Sq + kQueriesPerBlock - 1) / kQueriesPerBlock, a.H, a.B);
-  if (a.D == 64)
-    hipLaunchKernelGGL((flash_fwd_kernel<MASK, 64>), grid, dim3(kThreads), 0, stream, a);
-  else
-    hipLaunchKernelGGL((flash_fwd_kernel<MASK, 128>), grid, dim3(kThreads), 0, stream, a);
-  return (int)hipGetLastError();
+  const int64_t blocks256 = (int64_t)((a.Sq + 255) / 256) * a.H * a.B;
+  if (a.Sk <= 1024 || blocks256 < 768) return launch_waves<MASK, 4>(a, stream);
+  return launch_waves<MASK, 8>(a, stream);
 }
 
 }  // namespace

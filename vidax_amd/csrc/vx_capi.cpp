@@ -106,6 +106,10 @@ int32_t flash_check(const void* q, const void* k, const void* v, const void* out
   if ((rc = check_strides("k", ks, Sk)) != VX_OK) return rc;
   if ((rc = check_strides("v", vs, Sk)) != VX_OK) return rc;
   if ((rc = check_strides("out", os, Sq)) != VX_OK) return rc;
+  // the kernel forms key-row offsets within a 64-key tile in 32 bits
+  if (ks[1] > (int64_t(1) << 24) || vs[1] > (int64_t(1) << 24))
+    return fail(VX_ERR_UNSUPPORTED, "k/v sequence strides (%lld, %lld) above 2^24 elements are not supported",
+                (long long)ks[1], (long long)vs[1]);
   if (args != nullptr) {
     args->q = q;
     args->k = k;
