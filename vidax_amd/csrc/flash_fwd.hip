@@ -373,19 +373,10 @@ void flash_fwd_kernel(const FlashArgs a) {
       // fused scale in the exp argument.
       const int key0 = t * kBN;
       const lds_u8* mslot = lds + kMaskBuf + (t & (kMaskRing - 1)) * kMaskSlot;  // tile t's mask
-      uint32_t vbits[2][4];
       bool slow = key0 + kBN > kv_end;
       if (MASK & kMaskValid) {
-        bool hole = false;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            vbits[kb][g] = *(const VX_LDS uint32_t*)(mslot + kb * 32 + g * 8 + hf * 4);
-            // a zero byte anywhere in the word marks an invalid key
-            hole |= ((vbits[kb][g] - 0x01010101u) & ~vbits[kb][g] & 0x80808080u) != 0;
-          }
-        slow = slow || __builtin_amdgcn_ballot_w64(hole) != 0;
+        // lane l tests validity byte l of the tile: one LDS byte per lane
+        slow = slow || __builtin_amdgcn_ballot_w64(mslot[lane] == 0) != 0;
       }
       if (MASK & (kMaskBias | kMaskFull)) slow = true;
       stage(kg, klane, a.ks[1], min(t + kNB, n_tiles - 1), kKBuf + kb_next * kTileBytes);
@@ -394,6 +385,14 @@ void flash_fwd_kernel(const FlashArgs a) {
       float cc = c;
       if (slow) {
         cc = 1.0f;
+        // this lane's validity bytes: keys kb*32 + g*8 + hf*4 + 0..3
+        uint32_t vbits[2][4];
+        if (MASK & kMaskValid) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) vbits[kb][g] = *(const VX_LDS uint32_t*)(mslot + kb * 32 + g * 8 + hf * 4);
+        }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
