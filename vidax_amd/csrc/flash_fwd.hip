@@ -100,6 +100,9 @@ typedef VX_LDS unsigned char lds_u8;
 // kernel orders each copy itself with wait_vmem + a barrier before any wave
 // reads the destination buffer.
 __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_row) {
+  // M0 (the LDS destination) is set inside the statement and declared
+  // clobbered; the compiler places no other M0 access in these kernels
+  // (none appears in their assembly), so nothing of its own is lost.
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
                :
                : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_row))

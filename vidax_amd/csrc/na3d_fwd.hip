@@ -299,6 +299,9 @@ __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_row) {
   // Issued as inline assembly so the compiler does not wait for the copy
   // before every later LDS read; the kernel orders it with s_waitcnt and a
   // barrier before any wave reads the destination.
+  // M0 (the LDS destination) is set inside the statement and declared
+  // clobbered; the compiler places no other M0 access in these kernels
+  // (none appears in their assembly), so nothing of its own is lost.
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
                :
                : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_row))
