@@ -6,17 +6,17 @@
 // output: row max, row sum and the output rescale are per-lane scalars and the
 // two halves of the wave are combined with one v_permlane32_swap. Q stays in
 // registers as the B operand for the whole key loop. K and V tiles of 64 keys
-// are copied by the LDS DMA path (global_load_lds_dwordx4) into XOR-swizzled
-// LDS, three buffers each, two iterations ahead of their use, so their HBM /
-// L2 latency stays off the critical path; K is read back with ds_read_b128
-// (A operand of QK^T) and V with the gfx950 transpose read ds_read_b64_tr_b16
-// (A operand of O^T = V^T P^T).
+// are copied by the LDS DMA path (buffer_load_dwordx4 ... lds, issued by
+// waves 0-3) into XOR-swizzled LDS, three buffers each, two iterations ahead
+// of their use, so their HBM / L2 latency stays off the critical path; K is
+// read back with ds_read_b128 (A operand of QK^T) and V with the gfx950
+// transpose read ds_read_b64_tr_b16 (A operand of O^T = V^T P^T).
 //
 // Software pipeline: iteration t issues the MFMAs of QK^T(t+1) and of
 // PV(t-1) in one branch-free block together with the softmax VALU work of
-// tile t, interleaved slot by slot (one MFMA, the LDS read two slots ahead and
-// one score's exp per slot, fenced with sched_barrier), so the matrix cores and
-// the VALU of a wave run concurrently.
+// tile t, interleaved slot by slot (one MFMA, the LDS read three slots ahead
+// and one score's exp per slot, fenced with sched_barrier), so the matrix
+// cores and the VALU of a wave run concurrently.
 //
 // Softmax: scores are kept in log2 units (scale * log2(e) folded into the FMA
 // that feeds v_exp_f32). The probabilities of a tile are computed
@@ -56,19 +56,26 @@ struct FCfg {
   // In LDS a tile is D/64 half-planes of 64 keys x 128 bytes (d 0-63, then
   // d 64-127): one 1 KiB DMA copy fills 8 keys of one half-plane.
   static constexpr int kHalfBytes = kBN * 128;          // 8 KiB
-  static constexpr int kLoadsPerWave = kTileBytes / (WAVES * 1024);  // copies per wave per tile
+  // Waves 0 .. kCopyWaves-1 issue the tile copies, kLoadsPerWave each. A
+  // copy instruction holds its wave's issue for tens of cycles; with 8 waves
+  // only waves 0-3 (one per SIMD) copy, so each SIMD's other wave keeps the
+  // matrix core busy meanwhile.
+  static constexpr int kCopyWaves = WAVES == 8 ? 4 : WAVES;
+  static constexpr int kLoadsPerWave = kTileBytes / (kCopyWaves * 1024);
   static constexpr int kDB = D / 32;                    // 32-wide d blocks of O
   static constexpr int kDS = D / 16;                    // 16-deep d steps of QK^T
   static constexpr int kPV = 2 * 2 * kDB;               // MFMAs of PV per tile
   static constexpr int kQK = 2 * kDS;                   // MFMAs of QK^T per tile
   static constexpr int kSlots = kPV + kQK;              // 32 (16)
   static constexpr int kScoresPerSlot = 32 / kSlots;    // 1 (2)
+  // key masks: tile j's mask in slot j % kMaskRing; the ring holds the
+  // kNB masks in flight plus the one being read
+  static constexpr int kMaskRing = kNB < 4 ? 4 : 8;
 };
-// Key masks of the masked variants go through LDS like K: a ring of 4 slots
-// of 320 bytes (64 validity bytes, then 64 fp32 biases), slot j % 4 holding
-// tile j's mask, staged by wave 0 together with K_j.
+// Key masks of the masked variants go through LDS like K: a ring of slots
+// of 320 bytes (64 validity bytes, then 64 fp32 biases), staged by wave 0
+// together with K_j.
 constexpr int kMaskSlot = 320;
-constexpr int kMaskRing = 4;
 // Mask kinds (template argument, bits): validity bytes per key, additive bias
 // per key, additive bias per (query, key) of each head (read per query row
 // straight from global memory: meant for the short sequences that use it).
@@ -102,10 +109,35 @@ typedef VX_LDS unsigned char lds_u8;
 __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_row) {
   // M0 (the LDS destination) is set inside the statement and declared
   // clobbered; the compiler places no other M0 access in these kernels
-  // (none appears in their assembly), so nothing of its own is lost.
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+  // (none appears in their assembly), so nothing of its own is lost. One
+  // wait state separates the M0 write from the LDS DMA that reads it.
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                :
                : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_row))
+               : "memory", "m0");
+}
+
+// Raw buffer resource over [base, base + 4 GiB): no stride, untyped 32-bit
+// data, no range limit in practice (every offset used is below 2^31).
+typedef int i32x4_rsrc __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4_rsrc raw_rsrc(const void* base) {
+  const uint64_t addr = (uint64_t)(uintptr_t)base;
+  // the base is uniform: keep the resource in scalar registers
+  i32x4_rsrc r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
+  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(addr >> 32));  // 48-bit address; stride field 0
+  r[2] = -1;                                                            // num_records
+  r[3] = 0x00020000;                                                    // data format 32, raw access
+  return r;
+}
+
+// The same copy from a buffer resource: lane L fetches 16 bytes at byte
+// offset voff. A 32-bit offset per lane (not a 64-bit address) makes the
+// instruction cheaper to issue.
+__device__ __forceinline__ void lds_dma16_buf(i32x4_rsrc rsrc, uint32_t voff, uint32_t lds_row) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(lds_row))
                : "memory", "m0");
 }
 
@@ -126,6 +158,7 @@ void flash_fwd_kernel(const FlashArgs a) {
   constexpr int kWaves = C::kWaves, kThreads = C::kThreads, kNB = C::kNB;
   constexpr int kTileBytes = C::kTileBytes, kVBuf = C::kVBuf, kKBuf = C::kKBuf;
   constexpr int kSmemBytes = C::kSmemBytes, kMaskBuf = C::kMaskBuf, kLoadsPerWave = C::kLoadsPerWave;
+  constexpr int kMaskRing = C::kMaskRing, kCopyWaves = C::kCopyWaves;
   constexpr int kDB = C::kDB, kDS = C::kDS, kPV = C::kPV, kSlots = C::kSlots;
   constexpr bool MASKED = MASK != kMaskNone;
   constexpr int kMaskCopies = (MASK & kMaskValid ? 1 : 0) + (MASK & kMaskBias ? 1 : 0);
@@ -186,55 +219,48 @@ void flash_fwd_kernel(const FlashArgs a) {
   const int scol = lane & 7;
 
   // ---- global -> LDS staging of one 64-key tile on the LDS DMA path
-  // (global_load_lds_dwordx4): each wave instruction fills 8 consecutive
+  // (buffer_load_dwordx4 ... lds): each wave instruction fills 8 consecutive
   // half rows (1 KiB), lane L landing at byte 16*L, so lane L fetches the
   // global chunk that the swizzle places there. kLoadsPerWave instructions
-  // per wave per tile.
-  // Tiles that lie wholly below kv_end add a uniform tile offset to per-lane
-  // row pointers computed once; the tail tile clamps its rows to kv_end - 1.
+  // per copying wave per tile.
+  // Tiles that lie wholly below kv_end use per-lane offsets computed once;
+  // the tail tile clamps its rows to kv_end - 1.
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
-  // per-lane sources of the copies within tile 0: pointers with 8 waves
-  // (two copies per wave per tile), 32-bit element offsets from k / v with 4
-  // waves (four copies; a tile spans 63 rows of the key stride, well inside
-  // 32 bits) to save registers
-  using LaneSrc = std::conditional_t<WAVES == 8, const bf16*, int>;
+  // per-lane byte offsets of this wave's copies from the first row of a
+  // tile (a tile spans 63 rows of the key stride, at most 2^24 elements:
+  // well inside 32 bits); each tile's copies go through a buffer resource
+  // based at its first row
+  using LaneSrc = uint32_t;
   LaneSrc klane[kLoadsPerWave];
   LaneSrc vlane[kLoadsPerWave];
 #pragma unroll
   for (int p = 0; p < kLoadsPerWave; ++p) {
-    const int i = wave * kLoadsPerWave + p;
+    const int i = (wave % kCopyWaves) * kLoadsPerWave + p;
     const int r = 8 * (i & 7) + srow;
     const int col_el = (i >> 3) * 64 + ((scol ^ half_swizzle(r)) * 8);
-    if constexpr (WAVES == 8) {
-      klane[p] = kg + (int64_t)r * a.ks[1] + col_el;
-      vlane[p] = vg + (int64_t)r * a.vs[1] + col_el;
-    } else {
-      klane[p] = r * (int)a.ks[1] + col_el;
-      vlane[p] = r * (int)a.vs[1] + col_el;
-    }
+    klane[p] = (uint32_t)(r * (int)a.ks[1] + col_el) * 2u;
+    vlane[p] = (uint32_t)(r * (int)a.vs[1] + col_el) * 2u;
   }
-  auto stage = [&](const bf16* base, const LaneSrc (&lanep)[kLoadsPerWave], int64_t sstride, int t, int buf_off) {
+  // copy p of this wave for tile t
+  auto stage_one = [&](const bf16* base, const LaneSrc (&lanep)[kLoadsPerWave], int64_t sstride, int t, int buf_off,
+                       int p) {
+    if (wave >= kCopyWaves) return;
+    const int i = wave * kLoadsPerWave + p;
+    const i32x4_rsrc rs = raw_rsrc(base + (int64_t)(t * kBN) * sstride);
+    uint32_t voff;
     if ((t + 1) * kBN <= kv_end) {
-      const int64_t off = (int64_t)(t * kBN) * sstride;
-#pragma unroll
-      for (int p = 0; p < kLoadsPerWave; ++p) {
-        const bf16* src;
-        if constexpr (WAVES == 8)
-          src = lanep[p] + off;
-        else
-          src = base + off + lanep[p];
-        lds_dma16(src, lds_base + buf_off + (wave * kLoadsPerWave + p) * 1024);
-      }
+      voff = lanep[p];
     } else {
-#pragma unroll
-      for (int p = 0; p < kLoadsPerWave; ++p) {
-        const int i = wave * kLoadsPerWave + p;
-        const int r = 8 * (i & 7) + srow;
-        const int key = min(t * kBN + r, kv_end - 1);
-        const bf16* src = base + (int64_t)key * sstride + (i >> 3) * 64 + ((scol ^ half_swizzle(r)) * 8);
-        lds_dma16(src, lds_base + buf_off + i * 1024);
-      }
+      // tail tile: rows past kv_end repeat row kv_end - 1
+      const int r = 8 * (i & 7) + srow;
+      const int rr = min(r, kv_end - 1 - t * kBN);
+      voff = (uint32_t)(rr * (int)sstride + (i >> 3) * 64 + ((scol ^ half_swizzle(r)) * 8)) * 2u;
     }
+    lds_dma16_buf(rs, voff, lds_base + buf_off + i * 1024);
+  };
+  auto stage = [&](const bf16* base, const LaneSrc (&lanep)[kLoadsPerWave], int64_t sstride, int t, int buf_off) {
+#pragma unroll
+    for (int p = 0; p < kLoadsPerWave; ++p) stage_one(base, lanep, sstride, t, buf_off, p);
   };
 
   auto qk = [&](int buf_off, f32x16 (&S)[2]) {
@@ -307,43 +333,42 @@ void flash_fwd_kernel(const FlashArgs a) {
       if (lane < 16) lds_dma16(brow + j * kBN + lane * 4, slot + 64);
     }
   };
-  // At the top of an iteration: with three tiles per ring the previous
-  // iteration's DMA instructions may still be in flight; with two, the tiles
-  // read next were issued by the previous iteration, so all have to land.
+  // At the top of iteration t: the tiles it reads (K_{t+1}, V_{t-1}) were
+  // issued kNB - 1 iterations earlier; the copies of the last kNB - 2
+  // iterations may still be in flight.
   auto wait_prev = [&]() {
-    if (kNB == 2)
-      wait_vmem<0>();
-    else if (MASKED && wave == 0)
-      wait_vmem<2 * kLoadsPerWave + kMaskCopies>();
+    if (MASKED && wave == 0)
+      wait_vmem<(kNB - 2) * (2 * kLoadsPerWave + kMaskCopies)>();
     else
-      wait_vmem<2 * kLoadsPerWave>();
+      wait_vmem<(kNB - 2) * 2 * kLoadsPerWave>();
   };
 
   if (n_tiles > 0) {
     // Tile j of K lives in K buffer j % kNB and tile j of V in V buffer
     // j % kNB; V buffer kNB-1 stands in for "V_{-1}" (zeros, paired with P = 0
-    // in iteration 0). Iteration t issues K_{t+kNB} and V_{t+kNB-2}, into the
-    // buffers that the previous iteration finished reading.
-    // masks of the first tiles first: they are older than every copy the
-    // first iterations wait for
-    stage_mask(0);
-    stage_mask(min(1, n_tiles - 1));
-    if (kNB == 3) stage_mask(min(2, n_tiles - 1));
-    stage(kg, klane, a.ks[1], 0, kKBuf);
-    stage(kg, klane, a.ks[1], min(1, n_tiles - 1), kKBuf + kTileBytes);
-    if (kNB == 3) {
-      stage(kg, klane, a.ks[1], min(2, n_tiles - 1), kKBuf + 2 * kTileBytes);
-      stage(vg, vlane, a.vs[1], 0, kVBuf);
+    // in iteration 0). Iteration t issues K_{t+kNB}, its mask and
+    // V_{t+kNB-2}, into the buffers that the previous iteration finished
+    // reading; the prologue issues the same groups for t = -kNB .. -1, so
+    // that every wait below counts whole groups.
+#pragma unroll
+    for (int j = 0; j < kNB; ++j) {
+      stage(kg, klane, a.ks[1], min(j, n_tiles - 1), kKBuf + j * kTileBytes);
+      stage_mask(min(j, n_tiles - 1));
+      if (j >= 2) stage(vg, vlane, a.vs[1], min(j - 2, n_tiles - 1), kVBuf + (j - 2) * kTileBytes);
     }
 #pragma unroll
     for (int p = 0; p < kTileBytes / (kThreads * 16); ++p)
       *(VX_LDS u32x4*)(lds + kVBuf + (kNB - 1) * kTileBytes + (p * kThreads + threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
-    // K_0 (and K_1) have landed: the copies issued after them may still be
-    // in flight
-    if (kNB == 3)
-      wait_vmem<2 * kLoadsPerWave>();
-    else
-      wait_vmem<kLoadsPerWave>();
+    // K_0 has landed (with two tiles per ring, K_1 may still be in flight;
+    // with more, K_1 has landed too)
+    if (kNB == 2) {
+      if (MASKED && wave == 0)
+        wait_vmem<kLoadsPerWave + kMaskCopies>();
+      else
+        wait_vmem<kLoadsPerWave>();
+    } else {
+      wait_prev();
+    }
     __syncthreads();
     f32x16 S[2];
     qk(kKBuf, S);
@@ -367,8 +392,8 @@ void flash_fwd_kernel(const FlashArgs a) {
       // iteration's copies.
       wait_prev();
       __syncthreads();
-      const int kb_next = kb_cur == 0 ? kNB - 1 : kb_cur - 1;                    // t % kNB
-      const int vb_next = kNB == 2 ? kb_next : (vb_prev == 2 ? 1 : (vb_prev == 1 ? 0 : 2));  // (t+kNB-2) % kNB
+      const int kb_next = kb_cur == 0 ? kNB - 1 : kb_cur - 1;     // t % kNB
+      const int vb_next = vb_prev == 0 ? kNB - 1 : vb_prev - 1;  // (t+kNB-2) % kNB
 
       // ---- key masks. Tiles that hold a masked key (the tail tile, a
       // key_valid hole, any key_bias) take the scores to log2 units here,
@@ -382,6 +407,7 @@ void flash_fwd_kernel(const FlashArgs a) {
         slow = slow || __builtin_amdgcn_ballot_w64(mslot[lane] == 0) != 0;
       }
       if (MASK & (kMaskBias | kMaskFull)) slow = true;
+      // this iteration's copies: K_{t+kNB}, its mask and V_{t+kNB-2}
       stage(kg, klane, a.ks[1], min(t + kNB, n_tiles - 1), kKBuf + kb_next * kTileBytes);
       stage_mask(min(t + kNB, n_tiles - 1));
       stage(vg, vlane, a.vs[1], min(t + kNB - 2, n_tiles - 1), kVBuf + vb_next * kTileBytes);
@@ -417,7 +443,7 @@ void flash_fwd_kernel(const FlashArgs a) {
 
       // ---- one branch-free block of 32 slots: slot s issues one MFMA
       // (s < 16: PV(t-1) into O, s >= 16: QK^T(t+1) into Sn), the LDS read of
-      // the fragment two slots ahead, and one score's worth of softmax work for
+      // the fragment three slots ahead, and one score's worth of softmax work for
       // tile t (speculative against the current max). sched_barrier keeps the
       // slots in this order so MFMA and VALU work of a wave overlap.
       Sn[0] = f32x16{};
@@ -447,9 +473,10 @@ void flash_fwd_kernel(const FlashArgs a) {
         bf16x2 pk[16];
         fr[0] = frag(0);
         fr[1] = frag(1);
+        fr[2] = frag(2);
 #pragma unroll
         for (int s = 0; s < kSlots; ++s) {
-          if (s + 2 < kSlots) fr[s + 2] = frag(s + 2);
+          if (s + 3 < kSlots) fr[s + 3] = frag(s + 3);
           if (s < kPV) {
             const int db = s % kDB, j = (s / kDB) & 1, kb = s / (2 * kDB);
             O[db] = mfma32x32x16(fr[s], Pp[kb][j], O[db]);
