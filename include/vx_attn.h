@@ -140,7 +140,8 @@ int32_t vx_flash_attn_check(const void* q, const void* k, const void* v, const v
  * Tensors are contiguous (B, T, Hs, W, NH, D) bf16, 16-byte aligned.
  * Supported: head_dim 128 with 1 <= kt, kh, kw and min(kw, w) <= 57, or
  * head_dim 64 (the LTX-2.5 diffusion VAE's, src/vidax/models/ltx2_5/configs.py:
- * 194-203) with min(kw, w) <= 25; all sizes >= 1; batch, num_heads <= 65535.
+ * 194-203) with min(kw, w) <= 25; all sizes >= 1; batch, num_heads <= 65535;
+ * w * num_heads * head_dim < 2^30 (one row of tokens).
  */
 int32_t vx_na3d_fwd(const void* q, const void* k, const void* v, void* out, int32_t batch,
                     int32_t t, int32_t h, int32_t w, int32_t num_heads, int32_t head_dim,

@@ -98,6 +98,9 @@ def test_na3d_check():
     assert _na_check(D=96) == _lib.VX_ERR_UNSUPPORTED
     assert _na_check(T=0) == _lib.VX_ERR_INVALID_ARGUMENT
     assert _na_check(k=A + 1) == _lib.VX_ERR_INVALID_ARGUMENT
+    # one row of tokens (w * num_heads * head_dim elements) must stay below 2^30
+    assert _na_check(W=8192, NH=1023, D=128, kw=5) == _lib.VX_OK
+    assert _na_check(W=8192, NH=1024, D=128, kw=5) == _lib.VX_ERR_UNSUPPORTED
     assert _na_check(scale=float("nan")) == _lib.VX_ERR_INVALID_ARGUMENT
 
 

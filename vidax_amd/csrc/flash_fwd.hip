@@ -84,72 +84,7 @@ constexpr float kRescaleSlack = 8.0f;         // log2 units
 constexpr float kSumLimit = 256.0f;           // 2^kRescaleSlack
 constexpr float kNegBig = -1.0e30f;           // finite "no key seen yet" max
 
-// XOR swizzle of the 16-byte chunk index (0-7) within the 128-byte half row
-// of key r: the bit reversal of (r >> 1) & 7. The LDS has 64 four-byte banks
-// (256 bytes per cycle) and two consecutive half rows cover them once, so
-//  - the K reads (ds_read_b128, 16 lanes = keys 16i..16i+15 per cycle, one
-//    chunk index) hit 16 distinct 16-byte bank groups: the 8 even and the 8
-//    odd keys each see all 8 swizzles;
-//  - the V transpose reads (ds_read_b64_tr_b16, 32 lanes = keys 4i..4i+3,
-//    four chunks each, per cycle) hit 16 distinct groups: keys 4i, 4i+2 (and
-//    4i+1, 4i+3) differ in bit 2 of the swizzle.
-// Keys r and r + 8 differ only in bit 0 of the swizzle.
-__device__ __forceinline__ int half_swizzle(int r) {
-  return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
-}
-
 typedef VX_LDS unsigned char lds_u8;
-
-// One LDS DMA copy: 16 bytes per lane from `src` to LDS byte address
-// lds_row + 16 * lane (LDS base in M0). Issued as inline assembly so the
-// compiler does not treat every later LDS read as a possible reader of this
-// write (it would wait for the copy to land before the first such read); the
-// kernel orders each copy itself with wait_vmem + a barrier before any wave
-// reads the destination buffer.
-__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_row) {
-  // M0 (the LDS destination) is set inside the statement and declared
-  // clobbered; the compiler places no other M0 access in these kernels
-  // (none appears in their assembly), so nothing of its own is lost. One
-  // wait state separates the M0 write from the LDS DMA that reads it.
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_row))
-               : "memory", "m0");
-}
-
-// Raw buffer resource over [base, base + 4 GiB): no stride, untyped 32-bit
-// data, no range limit in practice (every offset used is below 2^31).
-typedef int i32x4_rsrc __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ i32x4_rsrc raw_rsrc(const void* base) {
-  const uint64_t addr = (uint64_t)(uintptr_t)base;
-  // the base is uniform: keep the resource in scalar registers
-  i32x4_rsrc r;
-  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
-  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(addr >> 32));  // 48-bit address; stride field 0
-  r[2] = -1;                                                            // num_records
-  r[3] = 0x00020000;                                                    // data format 32, raw access
-  return r;
-}
-
-// The same copy from a buffer resource: lane L fetches 16 bytes at byte
-// offset voff. A 32-bit offset per lane (not a 64-bit address) makes the
-// instruction cheaper to issue.
-__device__ __forceinline__ void lds_dma16_buf(i32x4_rsrc rsrc, uint32_t voff, uint32_t lds_row) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :
-               : "v"(voff), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(lds_row))
-               : "memory", "m0");
-}
-
-// s_waitcnt vmcnt(N), other counters untouched.
-template <int N>
-__device__ __forceinline__ void wait_vmem() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
-}
-
-// NaN test on the bit pattern (stays exact when the compiler may assume no NaNs).
-__device__ __forceinline__ bool is_nan_bits(float x) { return (__float_as_uint(x) & 0x7fffffffu) > 0x7f800000u; }
 
 template <int MASK, int D, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))

@@ -32,15 +32,6 @@ constexpr float kNegBig = -1.0e30f;
 
 __device__ __forceinline__ int row_swizzle(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
-// XOR swizzle of the 16-byte chunk index (0-7) within the 128-byte half row
-// of key slot r (the bit reversal of (r >> 1) & 7), for the pipelined kernel's
-// half-plane layout on the 64-bank LDS: any 16 consecutive slots (a K read of
-// 16 lanes) and any 4 consecutive slots x 4 chunks (a V transpose read of 32
-// lanes) fall on distinct 16-byte bank groups. Slots r and r + 8 differ only
-// in bit 0 of the swizzle.
-__device__ __forceinline__ int half_swizzle(int r) {
-  return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
-}
 
 __device__ __forceinline__ int window_start(int i, int len, int k) {
   return min(max(i - k / 2, 0), len - k);
@@ -295,27 +286,6 @@ struct PipeCfg {
   static_assert(kNS % kKeysPerCopy == 0 && kHalfL % 256 == 0, "whole copies per row, bank-aligned planes");
 };
 
-__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_row) {
-  // Issued as inline assembly so the compiler does not wait for the copy
-  // before every later LDS read; the kernel orders it with s_waitcnt and a
-  // barrier before any wave reads the destination.
-  // M0 (the LDS destination) is set inside the statement and declared
-  // clobbered; the compiler places no other M0 access in these kernels
-  // (none appears in their assembly), so nothing of its own is lost.
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_row))
-               : "memory", "m0");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmem() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
-}
-
-__device__ __forceinline__ bool is_nan_bits(float x) { return (__float_as_uint(x) & 0x7fffffffu) > 0x7f800000u; }
-
 template <int SEG, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
@@ -403,7 +373,10 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   constexpr int kGroups = C::kRowL / 1024;           // copies per LDS row
   constexpr int kGroupsPerHalf = C::kNS / C::kKeysPerCopy;
   const int srow = lane >> 3, scol = lane & 7;
-  int64_t dma_off[C::kCopiesPerWave];
+  // lane byte offset from the row's first token (w * NH * D < 2^30 elements,
+  // checked on the host, so it fits 31 bits); copies go through a buffer
+  // resource based at the row
+  uint32_t dma_voff[C::kCopiesPerWave];
   int dma_dst[C::kCopiesPerWave], dma_row[C::kCopiesPerWave];
 #pragma unroll
   for (int p = 0; p < C::kCopiesPerWave; ++p) {
@@ -413,7 +386,8 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
     const int pos = C::kKeysPerCopy * (g % kGroupsPerHalf) + srow;
     dma_row[p] = i / kGroups;
     dma_dst[p] = dma_row[p] * C::kRowL + g * 1024;
-    dma_off[p] = (int64_t)min(X_lo + pos, W - 1) * tok_stride + half * 64 + ((scol ^ half_swizzle(pos)) * 8);
+    dma_voff[p] =
+        (uint32_t)((int64_t)min(X_lo + pos, W - 1) * tok_stride + half * 64 + ((scol ^ half_swizzle(pos)) * 8)) * 2u;
   }
   // Box rows are walked with cursors (row index, its y in the box, its token
   // offset) that advance one row at a time and stop at the last row, so no
@@ -443,7 +417,7 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
     if (C::kRows == 2) advance(c);
 #pragma unroll
     for (int p = 0; p < C::kCopiesPerWave; ++p)
-      lds_dma16(base + (dma_row[p] ? rt1 : rt0) + dma_off[p], lds_base + slot_off + dma_dst[p]);
+      lds_dma16_buf(raw_rsrc(base + (dma_row[p] ? rt1 : rt0)), dma_voff[p], lds_base + slot_off + dma_dst[p]);
   };
 
   // ---- per-lane LDS offsets (half-plane 0; d 64-127 add kHalfL). K

@@ -165,6 +165,9 @@ int32_t na3d_check(const void* q, const void* k, const void* v, const void* out,
     return fail(VX_ERR_INVALID_ARGUMENT, "tensor of %lld elements per batch item is too large",
                 (long long)(tokens * NH * D));
   if ((int64_t)T * Hs * W > 0x7fffffff) return fail(VX_ERR_INVALID_ARGUMENT, "grid too large");
+  if ((int64_t)W * NH * D >= ((int64_t)1 << 30))
+    return fail(VX_ERR_UNSUPPORTED, "w x num_heads x head_dim = %lld elements per token row (must be below 2^30)",
+                (long long)((int64_t)W * NH * D));
   if (args != nullptr) {
     args->q = q;
     args->k = k;
