@@ -355,3 +355,56 @@ def test_flash_t5_relative_bias_head_dim_64(gpu):
                                 scale=1.0)
     torch.cuda.synchronize()
     _check(out, O.attention(O.bf16_round(q), k, v, scale=1.0, bias=bias), "t5")
+
+
+# ------------------------------------------- 256-query workgroups (8 waves)
+# The 8-wave kernel runs for long key sequences on large grids. B=1, H=24,
+# Sq=8192 (768 tiles of 256 queries) and Sk=1100 (17 key tiles and a 12-key
+# tail) select it while keeping the oracle cheap; sampled query rows (all
+# heads) are compared, including the first and last rows.
+EIGHT_WAVE_KINDS = ["plain", "kv_len", "key_valid", "key_bias", "all_key_masks", "full_bias"]
+
+
+@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("kind", EIGHT_WAVE_KINDS)
+def test_flash_eight_wave_variants(gpu, D, kind):
+    from vidax_amd import dot_product_attention, flash_attention
+    from vidax_amd.attention import flash_kernel_name
+    B, Sq, Sk, H = 1, 8192, 1100, 24
+    mask_kind = {"plain": 0, "kv_len": 0, "key_valid": 1, "key_bias": 2, "all_key_masks": 3, "full_bias": 5}[kind]
+    name = flash_kernel_name(B, Sq, Sk, H, D, mask_kind)
+    assert name.endswith(", 8>"), name
+    _say(f"flash 8 waves {name} kind={kind} B={B} Sq={Sq} Sk={Sk} H={H} D={D}")
+    seed = 90 + EIGHT_WAVE_KINDS.index(kind) + (0 if D == 128 else 10)
+    q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, D, seed)
+    rng = np.random.default_rng(seed + 1)
+    rows = _rows(Sq, 192, seed)
+    tq, tk, tv = _t(q, gpu), _t(k, gpu), _t(v, gpu)
+    kv_len = np.array([1037], dtype=np.int32)            # ends inside tile 16
+    valid = rng.random((B, Sk)) > 0.2
+    valid[:, 64:128] = False                             # one whole tile masked
+    key_bias = rng.standard_normal((B, Sk)).astype(np.float32)
+    key_bias[rng.random((B, Sk)) < 0.05] = -np.inf
+    dev = lambda a: torch.from_numpy(a).to(gpu)
+    if kind == "plain":
+        out = flash_attention(tq, tk, tv)
+        ref = O.attention(q[:, rows], k, v)
+    elif kind == "kv_len":
+        out = flash_attention(tq, tk, tv, kv_len=dev(kv_len))
+        ref = O.attention(q[:, rows], k, v, kv_len=kv_len)
+    elif kind == "key_valid":
+        out = flash_attention(tq, tk, tv, key_valid=dev(valid))
+        ref = O.attention(q[:, rows], k, v, key_valid=valid)
+    elif kind == "key_bias":
+        out = flash_attention(tq, tk, tv, key_bias=dev(key_bias))
+        ref = O.attention(q[:, rows], k, v, key_bias=key_bias)
+    elif kind == "all_key_masks":
+        out = flash_attention(tq, tk, tv, kv_len=dev(kv_len), key_valid=dev(valid), key_bias=dev(key_bias))
+        ref = O.attention(q[:, rows], k, v, kv_len=kv_len, key_valid=valid, key_bias=key_bias)
+    else:
+        # a (B, 1, Sq, Sk) bias shared by all heads plus a boolean key mask
+        bias = (0.5 * rng.standard_normal((B, 1, Sq, Sk))).astype(np.float32)
+        out = dot_product_attention(tq, tk, tv, bias=dev(bias), mask=dev(valid[:, None, None, :]))
+        ref = O.attention(q[:, rows], k, v, key_valid=valid, bias=bias[:, :, rows])
+    torch.cuda.synchronize()
+    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"8 waves {kind} D={D}")
