@@ -486,17 +486,14 @@ void flash_fwd_kernel(const FlashArgs a) {
   const float lt = halves_sum(l_run);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
   const int qi = qw0 + col;
+  u32x4 chunk[kDB][2];
+  pack_out_rows<kDB>(O, inv, chunk);  // all lanes: cross-lane exchange
   if (qi < a.Sq) {
     bf16* orow = og + (int64_t)qi * a.os[1];
 #pragma unroll
     for (int db = 0; db < kDB; ++db)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        bf16x4 ov;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ov[e] = (bf16)(O[db][g * 4 + e] * inv);
-        *(bf16x4*)(orow + db * 32 + g * 8 + hf * 4) = ov;
-      }
+      for (int pr = 0; pr < 2; ++pr) *(u32x4*)(orow + db * 32 + (2 * pr + hf) * 8) = chunk[db][pr];
   }
 }
 

@@ -229,17 +229,14 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
 
   const float lt = halves_sum(l_run);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  u32x4 chunk[4][2];
+  pack_out_rows<4>(O, inv, chunk);  // all lanes: cross-lane exchange
   if (q_in) {
     bf16* orow = og + token(t, yq, xq) * tok_stride;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        bf16x4 ov;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ov[e] = (bf16)(O[db][g * 4 + e] * inv);
-        *(bf16x4*)(orow + db * 32 + g * 8 + hf * 4) = ov;
-      }
+      for (int pr = 0; pr < 2; ++pr) *(u32x4*)(orow + db * 32 + (2 * pr + hf) * 8) = chunk[db][pr];
   }
 }
 
@@ -598,17 +595,14 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
 
   const float lt = halves_sum(l_run);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  u32x4 chunk[kDB][2];
+  pack_out_rows<kDB>(O, inv, chunk);  // all lanes: cross-lane exchange
   if (q_in) {
     bf16* orow = og + token(t, yq, xq) * tok_stride;
 #pragma unroll
     for (int db = 0; db < kDB; ++db)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        bf16x4 ov;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ov[e] = (bf16)(O[db][g * 4 + e] * inv);
-        *(bf16x4*)(orow + db * 32 + g * 8 + hf * 4) = ov;
-      }
+      for (int pr = 0; pr < 2; ++pr) *(u32x4*)(orow + db * 32 + (2 * pr + hf) * 8) = chunk[db][pr];
   }
 }
 

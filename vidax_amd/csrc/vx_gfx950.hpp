@@ -56,6 +56,35 @@ __device__ __forceinline__ float halves_sum(float x) {
   return lo + hi;
 }
 
+// Output rows of a wave's O^T accumulators (C layout above: lane l holds
+// column l%32 = one query, element 4g+e of block db = d db*32 + 8g +
+// (l/32)*4 + e), normalised by inv and packed to bf16 as 16-byte chunks:
+// one v_permlane32_swap per dword trades 4-d chunks between the half waves,
+// so that chunk (db, pr) of lane l holds d db*32 + 8*(2pr + l/32) + 0..7 of
+// its query. All 64 lanes must be active.
+template <int kDB>
+__device__ __forceinline__ void pack_out_rows(const f32x16 (&O)[kDB], float inv, u32x4 (&chunk)[kDB][2]) {
+#pragma unroll
+  for (int db = 0; db < kDB; ++db)
+#pragma unroll
+    for (int pr = 0; pr < 2; ++pr) {
+      bf16x4 lo, hi;  // d groups g = 2pr (lo) and 2pr + 1 (hi), 4 d each
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lo[e] = (bf16)(O[db][8 * pr + e] * inv);
+        hi[e] = (bf16)(O[db][8 * pr + 4 + e] * inv);
+      }
+      u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        const auto r = __builtin_amdgcn_permlane32_swap(a[w], b[w], false, false);
+        a[w] = r[0];
+        b[w] = r[1];
+      }
+      chunk[db][pr] = u32x4{a[0], a[1], b[0], b[1]};
+    }
+}
+
 __device__ __forceinline__ bf16x4 lds_read_tr16(const unsigned char* p) {
   s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p));
   return __builtin_bit_cast(bf16x4, r);
