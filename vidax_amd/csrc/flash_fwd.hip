@@ -403,6 +403,10 @@ void flash_fwd_kernel(const FlashArgs a) {
         };
         const float mneg = -m_run;
         const bf16x2 one2 = {(bf16)1.0f, (bf16)1.0f};
+        // The waves that issue no copies start their slots first; giving them
+        // issue priority while in the slots measured +0.7 % (the copying
+        // waves fill the gaps they leave).
+        if (wave >= kCopyWaves) __builtin_amdgcn_s_setprio(1);
         bf16x8 fr[kSlots];
         float pf[32];
         bf16x2 pk[16];
@@ -440,6 +444,8 @@ void flash_fwd_kernel(const FlashArgs a) {
                                                0, 1, 2, 3, 4, 5, 6, 7);
           }
       }
+
+      if (wave >= kCopyWaves) __builtin_amdgcn_s_setprio(0);
 
       // ---- rare: a probability may exceed 2^kRescaleSlack (the lane's tile
       // sum is above kSumLimit, inf or NaN; the first tile always lands here
