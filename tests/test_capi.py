@@ -257,3 +257,18 @@ def test_flash_kernel_name_follows_the_launch_rule():
     assert flash_kernel_name(2, 32760, 512, 40) == "flash_fwd_kernel<0, 128, 4>"      # short keys
     assert flash_kernel_name(1, 200, 200, 4, 64, 4) == "flash_fwd_kernel<4, 64, 4>"
     assert flash_kernel_name(3, 65536, 1025, 1) == "flash_fwd_kernel<0, 128, 8>"      # 768 tiles
+
+
+def test_kv_views_with_oversized_sequence_stride_are_copied():
+    """k/v views whose sequence stride exceeds the kernel's 2^24-element limit
+    are handed over as contiguous copies; other aligned views pass as they are."""
+    import torch
+    from vidax_amd.attention import _MAX_KV_SEQ_STRIDE, _aligned
+    big = _MAX_KV_SEQ_STRIDE + 8
+    buf = torch.zeros(big + 16, dtype=torch.bfloat16)
+    view = buf.as_strided((1, 2, 1, 8), (2 * big, big, 8, 1))
+    assert _aligned(view) is view                          # q: no sequence-stride limit
+    kv = _aligned(view, _MAX_KV_SEQ_STRIDE)
+    assert kv is not view and kv.is_contiguous() and kv.stride(1) == 8
+    small = torch.zeros((1, 4, 2, 64), dtype=torch.bfloat16)
+    assert _aligned(small, _MAX_KV_SEQ_STRIDE) is small

@@ -47,11 +47,19 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         raise ValueError("q, k and v must be on the same device")
 
 
-def _aligned(t: torch.Tensor) -> torch.Tensor:
-    """Tensor usable by the kernels: 16-byte aligned with strides in multiples of 8."""
-    if t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:3]):
-        return t
-    return t.contiguous()
+# The kernel copies k and v tiles with 32-bit offsets: their sequence stride
+# must stay within 2^24 elements (a contiguous (B, S, H, D) tensor has H * D).
+_MAX_KV_SEQ_STRIDE = 1 << 24
+
+
+def _aligned(t: torch.Tensor, max_seq_stride: Optional[int] = None) -> torch.Tensor:
+    """Tensor usable by the kernels: 16-byte aligned with strides in multiples
+    of 8 (and, for k and v, a sequence stride within the kernel's limit);
+    otherwise a contiguous copy."""
+    ok = t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:3])
+    if max_seq_stride is not None and t.stride(1) > max_seq_stride:
+        ok = False
+    return t if ok else t.contiguous()
 
 
 def _mask_rows(x: torch.Tensor, sk: int, dtype: torch.dtype, fill) -> torch.Tensor:
@@ -121,7 +129,8 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     if scale is None:
         scale = D ** -0.5
     scale = float(scale)
-    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    q = _aligned(q)
+    k, v = _aligned(k, _MAX_KV_SEQ_STRIDE), _aligned(v, _MAX_KV_SEQ_STRIDE)
     if out is None:
         out = torch.empty((B, Sq, H, D), dtype=q.dtype, device=q.device)
     elif out.shape != (B, Sq, H, D) or out.dtype != q.dtype or out.stride(-1) != 1:
