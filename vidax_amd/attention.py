@@ -133,8 +133,8 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     k, v = _aligned(k, _MAX_KV_SEQ_STRIDE), _aligned(v, _MAX_KV_SEQ_STRIDE)
     if out is None:
         out = torch.empty((B, Sq, H, D), dtype=q.dtype, device=q.device)
-    elif out.shape != (B, Sq, H, D) or out.dtype != q.dtype or out.stride(-1) != 1:
-        raise ValueError("out must be a (B, Sq, H, D) bf16 tensor with a contiguous head dim")
+    elif out.shape != (B, Sq, H, D) or out.dtype != q.dtype or out.stride(-1) != 1 or out.device != q.device:
+        raise ValueError("out must be a (B, Sq, H, D) bf16 tensor with a contiguous head dim, on q's device")
     dev = q.device
     kv_len_t = key_valid_t = key_bias_t = None
     stride = 0

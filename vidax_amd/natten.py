@@ -44,14 +44,17 @@ def na3d_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             raise ValueError(f"{name} must be a GPU tensor")
     if q.shape != k.shape or q.shape != v.shape:
         raise ValueError("q, k and v must have the same shape")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("q, k and v must be on the same device")
     if len(kernel_size) != 3:
         raise ValueError("kernel_size must be (kt, kh, kw)")
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     B, T, H, W, NH, HD = q.shape
     if out is None:
         out = torch.empty_like(q)
-    elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
-        raise ValueError("out must be a contiguous bf16 tensor shaped like q")
+    elif (out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous() or
+          out.device != q.device):
+        raise ValueError("out must be a contiguous bf16 tensor shaped like q, on q's device")
     stream = torch.cuda.current_stream(q.device).cuda_stream
     with torch.cuda.device(q.device):
         rc = _lib.lib().vx_na3d_fwd(
