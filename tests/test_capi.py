@@ -272,3 +272,16 @@ def test_kv_views_with_oversized_sequence_stride_are_copied():
     assert kv is not view and kv.is_contiguous() and kv.stride(1) == 8
     small = torch.zeros((1, 4, 2, 64), dtype=torch.bfloat16)
     assert _aligned(small, _MAX_KV_SEQ_STRIDE) is small
+
+
+def test_na3d_kernel_name_follows_the_launch_rule():
+    """The profiling-name helper mirrors the launcher's choice by the clamped x window."""
+    from vidax_amd.natten import na3d_kernel_name
+    assert na3d_kernel_name(80, 7) == "na3d_pipe_kernel<16, 128>"
+    assert na3d_kernel_name(80, 9, 64) == "na3d_pipe_kernel<16, 64>"
+    assert na3d_kernel_name(80, 11, 64) == "na3d_tall_kernel<64>"
+    assert na3d_kernel_name(80, 13) == "na3d_tall_kernel<128>"
+    assert na3d_kernel_name(12, 40) == "na3d_tall_kernel<128>"        # clamped to the grid width
+    assert na3d_kernel_name(80, 14) == "na3d_pipe_kernel<32, 128>"
+    assert na3d_kernel_name(80, 25, 64) == "na3d_pipe_kernel<32, 64>"
+    assert na3d_kernel_name(80, 27) == "na3d_wave_kernel"

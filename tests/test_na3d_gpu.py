@@ -48,6 +48,8 @@ NA_CASES = [
     ((1, 4, 17, 33, 1), (3, 5, 13), 42),
     ((2, 5, 9, 65, 2), (5, 3, 9), 43),     # ragged workgroup bricks along y and x
     ((1, 2, 20, 8, 1), (2, 9, 3), 44),
+    ((1, 3, 19, 37, 2), (3, 11, 11), 45),  # tall bricks (kw' 10-13), ragged along y (19 % 8) and x (37 % 16)
+    ((2, 4, 9, 23, 1), (3, 13, 10), 46),   # tall bricks, widest x window (13) clamped in y
 ]
 
 
@@ -69,6 +71,7 @@ NA_D64_CASES = [
     ((2, 5, 13, 21, 1), (3, 5, 5), 52),
     ((1, 12, 13, 24, 2), (11, 11, 11), 53),   # stage-5 window
     ((1, 3, 9, 40, 4), (3, 3, 25), 54),       # widest x window for head dim 64
+    ((1, 13, 21, 35, 2), (11, 11, 11), 55),   # stage-5 window, ragged tall bricks
 ]
 
 

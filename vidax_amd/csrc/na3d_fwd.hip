@@ -255,15 +255,24 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
 // (as in the flash kernel), so the matrix cores and the VALU work of a wave
 // overlap. With at most 80 KiB of LDS and 256 VGPRs two workgroups share a
 // CU. Head dims 128 and 64 (the LTX-2.5 diffusion VAE's) are instantiated.
+//
+// The tall geometry (TALL, SEG = 16, 9 < kw' <= 13) uses bricks of
+// 1 x 8 (y) x 16 (x) with waves of 8 y rows x 4 x columns: a wave's x union
+// (3 + kw' keys) still fits one 16-key segment, so a (11, 11, 11) window is
+// scored with 18 rows x 16 keys per plane instead of the 14 x 32 of the
+// 32-key segments.
 
-template <int SEG, int D>
+template <int SEG, int D, bool TALL = false>
 struct PipeCfg {
+  static_assert(!TALL || SEG == 16, "the tall geometry reads 16-key segments");
   static constexpr int kWaves = 4;
   static constexpr int kThreads = kWaves * 64;
-  static constexpr int kBrickY = 4, kBrickX = 32;
+  static constexpr int kBrickY = TALL ? 8 : 4, kBrickX = TALL ? 16 : 32;
+  static constexpr int kQX = kBrickX / kWaves;           // x columns per wave (32 / kQX y rows)
   static constexpr int kRB = D * 2;                      // bytes of one key
   static constexpr int kRows = SEG == 16 ? 2 : 1;        // key rows per step
-  static constexpr int kNS = SEG == 16 ? 40 : 64;        // key slots per LDS row (>= 24 + SEG)
+  // key slots per LDS row (>= kBrickX - kQX + SEG, a multiple of 8)
+  static constexpr int kNS = TALL ? 32 : (SEG == 16 ? 40 : 64);
   // An LDS key row is D/64 half-planes of kNS slots x 128 bytes (d 0-63,
   // then d 64-127); one 1 KiB DMA copy fills 8 slots of one half-plane.
   static constexpr int kHalfL = kNS * 128;               // one half-plane of a row
@@ -283,10 +292,10 @@ struct PipeCfg {
   static_assert(kNS % kKeysPerCopy == 0 && kHalfL % 256 == 0, "whole copies per row, bank-aligned planes");
 };
 
-template <int SEG, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
-  using C = PipeCfg<SEG, D>;
+template <int SEG, int D, bool TALL>
+__device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int n_xb) {
+  using C = PipeCfg<SEG, D, TALL>;
+  static_assert(C::kBrickX - C::kQX + SEG <= C::kNS, "a wave's segment stays inside the LDS row");
   __shared__ __attribute__((aligned(16))) unsigned char smem[C::kSmem];
   VX_LDS unsigned char* const lds = (VX_LDS unsigned char*)smem;
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
@@ -327,12 +336,12 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   const int nrows = kt * NY;
   const int n_steps = (nrows + C::kRows - 1) / C::kRows;
 
-  // ---- this wave's queries: y rows y0..y0+3, x columns xq0..xq0+7.
-  const int xq0 = x0 + 8 * wave;
-  const int ox = window_start(min(xq0, W - 1), W, kw) - X_lo;  // wave's first x slot, <= 24
+  // ---- this wave's queries: y rows y0..y0+kBrickY-1, x columns xq0..xq0+kQX-1.
+  const int xq0 = x0 + C::kQX * wave;
+  const int ox = window_start(min(xq0, W - 1), W, kw) - X_lo;  // wave's first x slot, <= kBrickX - kQX
 
   // ---- this lane's query and its window.
-  const int yq = y0 + col / 8, xq = xq0 + col % 8;
+  const int yq = y0 + col / C::kQX, xq = xq0 + col % C::kQX;
   const bool q_in = yq < Hs && xq < W;
   const int yqc = min(yq, Hs - 1), xqc = min(xq, W - 1);
   const int sy = window_start(yqc, Hs, kh) - Y_lo;
@@ -606,11 +615,33 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   }
 }
 
+template <int SEG, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
+  na3d_pipe_body<SEG, D, false>(a, n_yb, n_xb);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void na3d_tall_kernel(const Na3dArgs a, int n_yb, int n_xb) {
+  na3d_pipe_body<16, D, true>(a, n_yb, n_xb);
+}
+
 }  // namespace
 
 int launch_na3d_fwd(const Na3dArgs& a, void* stream) {
   if (a.D != 128 && a.D != 64) return (int)hipErrorNotSupported;
   hipStream_t st = (hipStream_t)stream;
+  if (a.kw > 9 && a.kw <= 13) {
+    const int n_yb = (a.Hs + 7) / 8;
+    const int n_xb = (a.W + 15) / 16;
+    dim3 grid((unsigned)a.T * n_yb * n_xb, a.NH, a.B);
+    if (a.D == 128)
+      hipLaunchKernelGGL((na3d_tall_kernel<128>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+    else
+      hipLaunchKernelGGL((na3d_tall_kernel<64>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+    return (int)hipGetLastError();
+  }
   if (a.kw <= 25) {
     const int n_yb = (a.Hs + 3) / 4;
     const int n_xb = (a.W + 31) / 32;

@@ -19,11 +19,14 @@ __all__ = ["neighborhood_attention_3d", "na3d_attention", "na3d_kernel_name"]
 
 def na3d_kernel_name(width: int, kernel_w: int, head_dim: int = 128) -> str:
     """Name of the kernel the library launches for this x window (profiling aid):
-    the pipelined row-streaming kernel with 16- or 32-key x segments up to
-    kw' = 25, the per-wave kernel above that (kw' = min(kw, W))."""
+    the pipelined row-streaming kernel with 16-key x segments up to kw' = 9,
+    its tall-brick form (8 y x 4 x queries per wave) up to kw' = 13, 32-key
+    segments up to kw' = 25, the per-wave kernel above that (kw' = min(kw, W))."""
     kw = min(int(kernel_w), int(width))
     if kw <= 9:
         return f"na3d_pipe_kernel<16, {head_dim}>"
+    if kw <= 13:
+        return f"na3d_tall_kernel<{head_dim}>"
     if kw <= 25:
         return f"na3d_pipe_kernel<32, {head_dim}>"
     return "na3d_wave_kernel"
