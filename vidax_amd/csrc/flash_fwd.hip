@@ -403,10 +403,13 @@ void flash_fwd_kernel(const FlashArgs a) {
         };
         const float mneg = -m_run;
         const bf16x2 one2 = {(bf16)1.0f, (bf16)1.0f};
-        // The waves that issue no copies start their slots first; giving them
-        // issue priority while in the slots measured +0.7 % (the copying
-        // waves fill the gaps they leave).
-        if (wave >= kCopyWaves) __builtin_amdgcn_s_setprio(1);
+        // Wave priority 1 while in the slots: with 8 waves for the waves that
+        // issue no copies (they start their slots first; the copying waves
+        // fill the gaps they leave: +0.7 %), with 4 waves (two workgroups per
+        // CU) for every wave, ahead of the other workgroup's wave while that
+        // one copies, waits or starts (+2-4 % at 512 keys).
+        constexpr bool kAllPrio = WAVES == 4;
+        if (kAllPrio || wave >= kCopyWaves) __builtin_amdgcn_s_setprio(1);
         bf16x8 fr[kSlots];
         float pf[32];
         bf16x2 pk[16];
@@ -445,7 +448,7 @@ void flash_fwd_kernel(const FlashArgs a) {
           }
       }
 
-      if (wave >= kCopyWaves) __builtin_amdgcn_s_setprio(0);
+      if (WAVES == 4 || wave >= kCopyWaves) __builtin_amdgcn_s_setprio(0);
 
       // ---- rare: a probability may exceed 2^kRescaleSlack (the lane's tile
       // sum is above kSumLimit, inf or NaN; the first tile always lands here
