@@ -524,6 +524,10 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     const float mneg = -m_run;
     bf16x8 fr[C::kSlots];
     float pf[16];
+    // wave priority 1 while in the slots, ahead of the other workgroup's
+    // wave on the SIMD while that one copies or waits (+1.5-2.5 % with the
+    // tall bricks, neutral with (3,7,7) windows)
+    __builtin_amdgcn_s_setprio(1);
     bf16x2 pk[8];
     fr[0] = frag(0);
     fr[1] = frag(1);
@@ -554,6 +558,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
       P[j] = __builtin_shufflevector(__builtin_shufflevector(pk[4 * j], pk[4 * j + 1], 0, 1, 2, 3),
                                      __builtin_shufflevector(pk[4 * j + 2], pk[4 * j + 3], 0, 1, 2, 3),
                                      0, 1, 2, 3, 4, 5, 6, 7);
+    __builtin_amdgcn_s_setprio(0);
     // rare: a probability may exceed 2^kRescaleSlack (the lane's chunk sum is
     // above kSumLimit, inf or NaN; the first chunk with a key in the window
     // always lands here) -> raise m_run to the chunk max, rescale O and l and
