@@ -65,7 +65,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const 
     const int c = lane + 64 * i;
     ss[i] = 0.f;
     if (live(c)) {
-      v[i] = *(const bf16x8*)(xr + c * 8);
+      v[i] = __builtin_nontemporal_load((const bf16x8*)(xr + c * 8));  // read once: streaming
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss[i] = __builtin_fmaf((float)v[i][e], (float)v[i][e], ss[i]);
     }
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const 
 #pragma unroll
   for (int i = 0; i < NCHUNK; ++i) {
     const int c = lane + 64 * i;
-    if (live(c)) *(bf16x8*)(orow + c * 8) = v[i];
+    if (live(c)) __builtin_nontemporal_store(v[i], (bf16x8*)(orow + c * 8));  // written once
   }
 }
 
