@@ -38,6 +38,10 @@ WORKLOADS = {
                           "joint self-attention B=1 H=24 S=33*45*80+256, last 0-200 keys masked"),
     "na3d_21x45x80_H24": ("na3d", dict(B=1, T=21, Hs=45, W=80, NH=24, kernel=(3, 7, 7), seed=3),
                           "3D neighbourhood attention 21x45x80, window (3,7,7), B=1 NH=24 D=128"),
+    "na3d_stage5_33x88x160_H4_D64": ("na3d", dict(B=1, T=33, Hs=88, W=160, NH=4, D=64, kernel=(11, 11, 11),
+                                                  seed=6),
+                                     "3D neighbourhood attention 33x88x160, window (11,11,11), B=1 NH=4 D=64 "
+                                     "(LTX-2.5 VAE stage 5 head layout)"),
     "qk_norm_rope_L32760_H40": ("prologue", dict(B=1, grid=(21, 30, 52), H=40, seed=5),
                                 "q and k RMSNorm(5120) + 3D RoPE, B=1 L=32760 (21x30x52) H=40 D=128"),
 }
@@ -85,7 +89,7 @@ def _flash_work(p, valid_keys):
 
 
 def _na3d_work(p):
-    B, T, Hs, W, NH, D = p["B"], p["T"], p["Hs"], p["W"], p["NH"], 128
+    B, T, Hs, W, NH, D = p["B"], p["T"], p["Hs"], p["W"], p["NH"], p.get("D", 128)
     kt, kh, kw = (min(p["kernel"][0], T), min(p["kernel"][1], Hs), min(p["kernel"][2], W))
     n = T * Hs * W
     flops = 4.0 * B * NH * n * kt * kh * kw * D
@@ -139,9 +143,11 @@ def _cpu_baseline(kind, p, budget_s=12.0):
         gbs = 2.0 * 2 * S * L * reps / el / 1e9
         sample = f"oracle fp32 (numpy) RMSNorm+RoPE of {S} tokens x {L}, {reps} reps, {el:.1f} s"
         return {"value": round(gbs, 3), "unit": "GB/s", "cores": int(threads), "kind": "port", "sample": sample}
-    # na3d: a slab of T rows with the full H x W plane, all heads
-    T = min(3, p["T"])
-    shape = (1, T, p["Hs"], p["W"], 2, 128)
+    # na3d: a slab of up to 3 planes of the H x W grid (24 rows of it for
+    # windows wider than 8 x 8), two heads
+    T, D = min(3, p["T"]), p.get("D", 128)
+    Hs = p["Hs"] if p["kernel"][1] * p["kernel"][2] <= 64 else min(p["Hs"], 24)
+    shape = (1, T, Hs, p["W"], 2, D)
     q = O.bf16_round(rng.standard_normal(shape, dtype=np.float32))
     k = O.bf16_round(rng.standard_normal(shape, dtype=np.float32))
     v = O.bf16_round(rng.standard_normal(shape, dtype=np.float32))
@@ -152,9 +158,9 @@ def _cpu_baseline(kind, p, budget_s=12.0):
         el = time.perf_counter() - t0
         if el >= budget_s or reps >= 200:
             break
-    kt, kh, kw = (min(p["kernel"][0], T), min(p["kernel"][1], p["Hs"]), min(p["kernel"][2], p["W"]))
-    flops = 4.0 * 2 * T * p["Hs"] * p["W"] * kt * kh * kw * 128 * reps
-    sample = f"oracle fp32 NA3D on a (1,{T},{p['Hs']},{p['W']},2,128) slab, {reps} reps, {el:.1f} s"
+    kt, kh, kw = (min(p["kernel"][0], T), min(p["kernel"][1], Hs), min(p["kernel"][2], p["W"]))
+    flops = 4.0 * 2 * T * Hs * p["W"] * kt * kh * kw * D * reps
+    sample = f"oracle fp32 NA3D on a (1,{T},{Hs},{p['W']},2,{D}) slab, {reps} reps, {el:.1f} s"
     return {"value": round(flops / el / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads),
             "kind": "port", "sample": sample}
 
@@ -247,8 +253,9 @@ def main(argv=None):
     else:
         g = torch.Generator(device=dev)
         g.manual_seed(p["seed"])
-        shape = (p["B"], p["T"], p["Hs"], p["W"], p["NH"], 128)
-        q = (torch.randn(shape, generator=g, device=dev) * 128 ** -0.5).to(torch.bfloat16)
+        D = p.get("D", 128)
+        shape = (p["B"], p["T"], p["Hs"], p["W"], p["NH"], D)
+        q = (torch.randn(shape, generator=g, device=dev) * D ** -0.5).to(torch.bfloat16)
         k = torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)
         v = torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)
         out = torch.empty_like(q)
@@ -257,7 +264,7 @@ def main(argv=None):
 
         def step():
             na3d_attention(q, k, v, p["kernel"], out=out)
-        kernel_name = vidax_amd.natten.na3d_kernel_name(p["W"], p["kernel"][2])
+        kernel_name = vidax_amd.natten.na3d_kernel_name(p["W"], p["kernel"][2], D)
 
     for _ in range(args.warmup):
         step()
@@ -284,6 +291,11 @@ def main(argv=None):
         roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                     "traffic": _traffic(kernel_name, args.workload)}
+    elif flops / bytes_ > PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9):
+        # a wide window (e.g. 11^3) lies right of the ridge: matrix-core bound
+        roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                    "traffic": _traffic(kernel_name, args.workload)}
     else:
         roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
@@ -307,7 +319,7 @@ def main(argv=None):
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic N(0,1) bf16 inputs resident in HBM",
-        "config": {"workload": desc, "B": p["B"], "heads": p.get("H", p.get("NH")), "head_dim": 128,
+        "config": {"workload": desc, "B": p["B"], "heads": p.get("H", p.get("NH")), "head_dim": p.get("D", 128),
                    "kernel": kernel_name},
         "pct_bf16_mfma_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
         "ms_per_call": round(ms, 4),
