@@ -1,7 +1,9 @@
-// Non-causal flash attention forward for gfx950, bf16 in/out, D = 128.
+// Non-causal flash attention forward for gfx950, bf16 in/out, D = 128 or 64.
 //
 // Work decomposition: one workgroup of 8 waves per (256-query tile, head,
-// batch item); each wave owns 32 query rows, two waves per SIMD. The wave
+// batch item), or of 4 waves per 128-query tile for short key sequences and
+// small grids (two workgroups per CU); each wave owns 32 query rows, two
+// waves per SIMD. The wave
 // computes S^T = K Q^T so that every lane owns one query column of the MFMA
 // output: row max, row sum and the output rescale are per-lane scalars and the
 // two halves of the wave are combined with one v_permlane32_swap. Q stays in
@@ -257,7 +259,8 @@ void flash_fwd_kernel(const FlashArgs a) {
                             : nullptr;
   const float* brow = (MASK & kMaskBias) ? a.key_bias + (int64_t)b * a.key_mask_stride : nullptr;
   // Wave 0 stages tile j's mask (64 validity bytes: lanes 0-3; 64 biases:
-  // lanes 0-15) into mask slot j % 4. Mask rows hold whole 64-key tiles.
+  // lanes 0-15) into mask slot j % kMaskRing. Mask rows hold whole 64-key
+  // tiles.
   auto stage_mask = [&](int j) {
     if (!MASKED || wave != 0) return;
     const uint32_t slot = lds_base + kMaskBuf + (j & (kMaskRing - 1)) * kMaskSlot;
@@ -491,7 +494,8 @@ void flash_fwd_kernel(const FlashArgs a) {
     pv(kVBuf + vb_prev * kTileBytes, Pp, O);
   }
 
-  // ---- epilogue: normalise and store (lane holds 4 consecutive d per group).
+  // ---- epilogue: normalise, pack to 16-byte chunks of 8 consecutive d
+  // (pack_out_rows) and store.
   const float lt = halves_sum(l_run);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
   const int qi = qw0 + col;
