@@ -408,3 +408,28 @@ def test_flash_eight_wave_variants(gpu, D, kind):
         ref = O.attention(q[:, rows], k, v, key_valid=valid, bias=bias[:, :, rows])
     torch.cuda.synchronize()
     _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"8 waves {kind} D={D}")
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_flash_eight_wave_two_batch_items(gpu, D):
+    """8-wave kernel with B=2: per-item kv_len (one inside a tile, one
+    below Sk by a whole tile and more) and key_valid holes, sampled rows of
+    both items."""
+    from vidax_amd import flash_attention
+    from vidax_amd.attention import flash_kernel_name
+    B, Sq, Sk, H = 2, 4096, 1100, 24
+    name = flash_kernel_name(B, Sq, Sk, H, D, 1)
+    assert name.endswith(", 8>"), name
+    _say(f"flash 8 waves B=2 {name} Sq={Sq} Sk={Sk} H={H} D={D}")
+    seed = 120 + (0 if D == 128 else 1)
+    q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, D, seed)
+    rng = np.random.default_rng(seed + 1)
+    kv_len = np.array([1037, 655], dtype=np.int32)
+    valid = rng.random((B, Sk)) > 0.25
+    valid[1, 128:192] = False
+    rows = _rows(Sq, 160, seed)
+    dev = lambda a: torch.from_numpy(a).to(gpu)
+    out = flash_attention(_t(q, gpu), _t(k, gpu), _t(v, gpu), kv_len=dev(kv_len), key_valid=dev(valid))
+    torch.cuda.synchronize()
+    ref = O.attention(q[:, rows], k, v, kv_len=kv_len, key_valid=valid)
+    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"8 waves B=2 D={D}")
