@@ -50,6 +50,8 @@ NA_CASES = [
     ((1, 2, 20, 8, 1), (2, 9, 3), 44),
     ((1, 3, 19, 37, 2), (3, 11, 11), 45),  # tall bricks (kw' 10-13), ragged along y (19 % 8) and x (37 % 16)
     ((2, 4, 9, 23, 1), (3, 13, 10), 46),   # tall bricks, widest x window (13) clamped in y
+    ((1, 3, 5, 40, 2), (3, 3, 7), 47),     # x bricks 32-63: waves 1-3 hold no query (x >= 40)
+    ((2, 2, 7, 20, 1), (2, 3, 9), 48),     # one x brick, wave 3 (x 24-31) empty; kw' = 9
 ]
 
 
@@ -72,6 +74,7 @@ NA_D64_CASES = [
     ((1, 12, 13, 24, 2), (11, 11, 11), 53),   # stage-5 window
     ((1, 3, 9, 40, 4), (3, 3, 25), 54),       # widest x window for head dim 64
     ((1, 13, 21, 35, 2), (11, 11, 11), 55),   # stage-5 window, ragged tall bricks
+    ((1, 3, 12, 40, 2), (3, 9, 9), 56),       # empty waves at the ragged x edge
 ]
 
 

@@ -343,6 +343,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   // ---- this lane's query and its window.
   const int yq = y0 + col / C::kQX, xq = xq0 + col % C::kQX;
   const bool q_in = yq < Hs && xq < W;
+  const bool wave_in = y0 < Hs && xq0 < W;  // wave-uniform: some query of the wave is in the grid
   const int yqc = min(yq, Hs - 1), xqc = min(xq, W - 1);
   const int sy = window_start(yqc, Hs, kh) - Y_lo;
   const int sx = window_start(xqc, W, kw) - X_lo - ox;  // in [0, SEG - kw]
@@ -515,6 +516,13 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 
     const VX_LDS unsigned char* kb = lds + C::kK + ((s + 1) & 1) * C::kSlot;  // K of chunk s+1
     const VX_LDS unsigned char* vb = lds + C::kV + ((s + 1) & 1) * C::kSlot;  // V of chunk s-1
+    if (!wave_in) {
+      // no query of this wave is inside the grid (the ragged x or y edge):
+      // it only copies its share of the rows
+      P[0] = bf16x8{};
+      P[1] = bf16x8{};
+      return;
+    }
     // PV fragment f < kPV: key half j = f / kDB, d block f % kDB; then QK^T.
     auto frag = [&](int i) -> bf16x8 {
       return i < C::kPV ? vfrag(vb, i / kDB, i % kDB) : kfrag(kb, i - C::kPV);
