@@ -9,8 +9,9 @@
 // two halves of the wave are combined with one v_permlane32_swap. Q stays in
 // registers as the B operand for the whole key loop. K and V tiles of 64 keys
 // are copied by the LDS DMA path (buffer_load_dwordx4 ... lds, issued by
-// waves 0-3) into XOR-swizzled LDS, three buffers each, two iterations ahead
-// of their use, so their HBM / L2 latency stays off the critical path; K is
+// waves 0-3) into XOR-swizzled LDS, three buffers each issued two iterations
+// ahead of their use (two buffers, one iteration ahead, in 4-wave
+// workgroups), so their HBM / L2 latency stays off the critical path; K is
 // read back with ds_read_b128 (A operand of QK^T) and V with the gfx950
 // transpose read ds_read_b64_tr_b16 (A operand of O^T = V^T P^T).
 //

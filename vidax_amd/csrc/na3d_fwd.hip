@@ -1,18 +1,26 @@
 // 3D neighbourhood attention forward for gfx950 (NATTEN semantics with
-// boundary-clamped windows), bf16 in/out, D = 128.
+// boundary-clamped windows), bf16 in/out, head dim 128 or 64.
 //
-// Each wave owns a query brick of 1 (t) x 4 (y) x 8 (x) = 32 queries of one
-// head. Because the brick spans a single t, every query in it shares the t
-// window, and the union of the bricks' windows is a (kt', ny, nx) box of
-// keys with ny <= 3 + kh' and nx <= 7 + kw'. The wave walks that box in
-// chunks of 32 keys, laid out as (t', y') rows of SEG = round_up(nx, 16)
-// x-positions, so every 16-key half chunk lies inside one (t', y') row. Per
-// chunk it computes S^T = K Q^T with bf16 MFMA (K fragments loaded straight
-// from global memory), masks every (query, key) pair outside the query's own
-// window to -inf, runs the same lazy-rescale online softmax as the flash
-// kernel, and accumulates O^T += V^T P^T with V staged through a
-// wave-private, double-buffered LDS slot and read back with the transpose
-// read. Waves never synchronise with each other.
+// Three kernels, chosen by the clamped x window kw' (launch_na3d_fwd):
+// - na3d_pipe_kernel<SEG, D> (kw' <= 9 or 13 < kw' <= 25): a workgroup of 4
+//   waves owns a 1 (t) x 4 (y) x 32 (x) query brick of one head and streams
+//   the union of its windows, kt' x NY key rows (t', y'), through LDS with
+//   the DMA copy path; each wave reads the SEG-wide x window its 4 x 8
+//   queries need, 32 keys per step, and runs the flash kernel's software
+//   pipeline (QK^T of the next chunk and PV of the previous one interleaved
+//   with the masking and lazy-rescale softmax of the current one).
+// - na3d_tall_kernel<D> (9 < kw' <= 13): the same body on 1 x 8 x 16 bricks
+//   with waves of 8 y x 4 x queries, so that a wave's x window still fits a
+//   16-key segment.
+// - na3d_wave_kernel (25 < kw' <= 57, D = 128): each wave owns a
+//   1 x 4 x 8 brick on its own and walks its (kt', ny, nx) key box in chunks
+//   of 32 keys, laid out as (t', y') rows of SEG = round_up(nx, 16)
+//   x-positions, with K fragments loaded straight from global memory and V
+//   staged through a wave-private, double-buffered LDS slot; its waves never
+//   synchronise with each other.
+// In all three, every (query, key) pair outside the query's own window is
+// set to -inf before the exponent, so each query attends exactly its
+// kt' x kh' x kw' window.
 #include "vx_gfx950.hpp"
 #include "vx_kernels.h"
 
