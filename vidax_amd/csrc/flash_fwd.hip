@@ -84,6 +84,7 @@ constexpr int kMaskSlot = 320;
 constexpr int kMaskNone = 0, kMaskValid = 1, kMaskBias = 2, kMaskFull = 4;
 constexpr float kRescaleSlack = 8.0f;         // log2 units
 constexpr float kSumLimit = 256.0f;           // 2^kRescaleSlack
+static_assert(kSumLimit == (float)(1 << (int)kRescaleSlack), "the tile-sum limit is 2^slack");
 constexpr float kNegBig = -1.0e30f;           // finite "no key seen yet" max
 
 typedef VX_LDS unsigned char lds_u8;
