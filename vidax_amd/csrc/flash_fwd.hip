@@ -201,9 +201,29 @@ void flash_fwd_kernel(const FlashArgs a) {
     for (int p = 0; p < kLoadsPerWave; ++p) stage_one(base, lanep, sstride, t, buf_off, p);
   };
 
+  // A per-key bias enters the scores through the QK^T accumulator: it starts
+  // at bias / scale for the lane's keys kb*32 + g*8 + hf*4 + 0..3 of tile j
+  // (the tile's mask slot, in LDS by then), so that scale * log2(e) * S is
+  // the scaled logit plus bias * log2(e) and bias tiles stay on the fast path.
+  const float inv_scale = 1.0f / a.scale;
+  auto acc_init = [&](int j, f32x16 (&S)[2]) {
+    if (MASK & kMaskBias) {
+      const lds_u8* bslot = lds + kMaskBuf + (j & (kMaskRing - 1)) * kMaskSlot + 64;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 b = *(const VX_LDS f32x4*)(bslot + (kb * 32 + g * 8 + hf * 4) * 4) * inv_scale;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) S[kb][g * 4 + e] = b[e];
+        }
+    } else {
+      S[0] = f32x16{};
+      S[1] = f32x16{};
+    }
+  };
   auto qk = [&](int buf_off, f32x16 (&S)[2]) {
-    S[0] = f32x16{};
-    S[1] = f32x16{};
+    acc_init(0, S);
     const lds_u8* kb0 = lds + buf_off;
 #pragma unroll
     for (int ds = 0; ds < kDS; ++ds) {
@@ -345,7 +365,7 @@ void flash_fwd_kernel(const FlashArgs a) {
         // lane l tests validity byte l of the tile: one LDS byte per lane
         slow = slow || __builtin_amdgcn_ballot_w64(mslot[lane] == 0) != 0;
       }
-      if (MASK & (kMaskBias | kMaskFull)) slow = true;
+      if (MASK & kMaskFull) slow = true;
       // this iteration's copies: K_{t+kNB}, its mask and V_{t+kNB-2}
       stage(kg, klane, a.ks[1], min(t + kNB, n_tiles - 1), kKBuf + kb_next * kTileBytes);
       stage_mask(min(t + kNB, n_tiles - 1));
@@ -367,7 +387,6 @@ void flash_fwd_kernel(const FlashArgs a) {
           for (int g = 0; g < 4; ++g) {
             const int kbase = key0 + kb * 32 + g * 8 + hf * 4;
             f32x4 bias = {0.f, 0.f, 0.f, 0.f};
-            if (MASK & kMaskBias) bias = *(const VX_LDS f32x4*)(mslot + 64 + (kbase - key0) * 4) * kLog2e;
             if (kFull) bias += *(const f32x4*)(frow + kbase) * kLog2e;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -389,8 +408,6 @@ void flash_fwd_kernel(const FlashArgs a) {
       // score's exp into every slot (and no slower with 4 waves). In 8-wave
       // workgroups the VALU block follows the MFMAs, in 4-wave workgroups it
       // precedes them.
-      Sn[0] = f32x16{};
-      Sn[1] = f32x16{};
       float l_tile = 0.f;
       {
         const lds_u8* kb0 = lds + kKBuf + kb_cur * kTileBytes;
@@ -444,6 +461,7 @@ void flash_fwd_kernel(const FlashArgs a) {
           __builtin_amdgcn_sched_barrier(0);
         };
         if (WAVES == 4) softmax_block();
+        acc_init(t + 1, Sn);  // read by the QK^T slots (16 and on)
 #pragma unroll
         for (int s = 0; s < kSlots; ++s) {
           if (s + 3 < kSlots) fr[s + 3] = frag(s + 3);
