@@ -550,24 +550,59 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     // kSlots slots: slot i issues one MFMA (i < kPV: PV(s-1), else QK^T(s+1)),
     // the LDS read two slots ahead, and the mask + exp of kScoresPerSlot
     // scores of chunk s.
+    if constexpr (TALL && D == 64) {
+      // tall bricks at head dim 64: the MFMA block, then the masking and
+      // softmax block, so the two waves of a SIMD alternate between them
+      // (+1.6 % at the (11, 11, 11) window; at head dim 128 and in the
+      // 1 x 4 x 32 bricks the per-slot interleave measured as fast or faster)
 #pragma unroll
-    for (int i = 0; i < C::kSlots; ++i) {
-      if (i + 2 < C::kSlots) fr[i + 2] = frag(i + 2);
-      if (i < C::kPV)
-        O[i % kDB] = mfma32x32x16(fr[i], Pp[i / kDB], O[i % kDB]);
-      else
-        Sn = mfma32x32x16(fr[i], qr[i - C::kPV], Sn);
-#pragma unroll
-      for (int u = 0; u < C::kScoresPerSlot; ++u) {
-        const int e = i * C::kScoresPerSlot + u;
-        S[e] = __builtin_fminf(__builtin_fminf(S[e], xlim[e]), rlim[e >> 3]);
-        pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, mneg));
-        if (e & 1) {
-          pk[e >> 1] = bf16x2{(bf16)pf[e - 1], (bf16)pf[e]};
-          l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[e >> 1], one2, l_tile, false);
-        }
+      for (int i = 0; i < C::kSlots; ++i) {
+        if (i + 2 < C::kSlots) fr[i + 2] = frag(i + 2);
+        if (i < C::kPV)
+          O[i % kDB] = mfma32x32x16(fr[i], Pp[i / kDB], O[i % kDB]);
+        else
+          Sn = mfma32x32x16(fr[i], qr[i - C::kPV], Sn);
+        __builtin_amdgcn_sched_barrier(0);
       }
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int e = 8 * g + i;
+          S[e] = __builtin_fminf(__builtin_fminf(S[e], xlim[e]), rlim[e >> 3]);
+          pf[e] = __builtin_fmaf(S[e], c2, mneg);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pf[8 * g + i] = fast_exp2(pf[8 * g + i]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pk[4 * g + i] = bf16x2{(bf16)pf[8 * g + 2 * i], (bf16)pf[8 * g + 2 * i + 1]};
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[i], one2, l_tile, false);
       __builtin_amdgcn_sched_barrier(0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < C::kSlots; ++i) {
+        if (i + 2 < C::kSlots) fr[i + 2] = frag(i + 2);
+        if (i < C::kPV)
+          O[i % kDB] = mfma32x32x16(fr[i], Pp[i / kDB], O[i % kDB]);
+        else
+          Sn = mfma32x32x16(fr[i], qr[i - C::kPV], Sn);
+#pragma unroll
+        for (int u = 0; u < C::kScoresPerSlot; ++u) {
+          const int e = i * C::kScoresPerSlot + u;
+          S[e] = __builtin_fminf(__builtin_fminf(S[e], xlim[e]), rlim[e >> 3]);
+          pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, mneg));
+          if (e & 1) {
+            pk[e >> 1] = bf16x2{(bf16)pf[e - 1], (bf16)pf[e]};
+            l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[e >> 1], one2, l_tile, false);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
