@@ -433,3 +433,29 @@ def test_flash_eight_wave_two_batch_items(gpu, D):
     torch.cuda.synchronize()
     ref = O.attention(q[:, rows], k, v, kv_len=kv_len, key_valid=valid)
     _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"8 waves B=2 D={D}")
+
+
+@pytest.mark.parametrize("shape", [(2, 300, 700, 3), (1, 8192, 1100, 24)], ids=["4 waves", "8 waves"])
+@pytest.mark.parametrize("D", [128, 64])
+def test_flash_dominant_key_bias(gpu, shape, D):
+    """A key bias that dominates the logits (+-40, runs of -inf in the middle
+    of the sequence as in Cosmos3's text padding) with a small scale (0.02):
+    the bias enters the QK^T accumulator as bias / scale (up to 2000), and
+    the reference point has to follow the bias, not q.k."""
+    from vidax_amd import flash_attention
+    from vidax_amd.attention import flash_kernel_name
+    B, Sq, Sk, H = shape
+    name = flash_kernel_name(B, Sq, Sk, H, D, 2)
+    _say(f"flash dominant key bias {name} B={B} Sq={Sq} Sk={Sk} H={H} D={D}")
+    seed = 130 + (0 if D == 128 else 1) + (0 if Sq < 1000 else 2)
+    q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, D, seed)
+    rng = np.random.default_rng(seed + 1)
+    bias = (40.0 * rng.uniform(-1.0, 1.0, (B, Sk))).astype(np.float32)
+    bias[:, Sk // 3:Sk // 3 + 150] = -np.inf          # a padded run mid-sequence
+    bias[rng.random((B, Sk)) < 0.05] = -np.inf
+    rows = _rows(Sq, min(Sq, 160), seed)
+    out = flash_attention(_t(q, gpu), _t(k, gpu), _t(v, gpu), scale=0.02,
+                          key_bias=torch.from_numpy(bias).to(gpu))
+    torch.cuda.synchronize()
+    ref = O.attention(q[:, rows], k, v, scale=0.02, key_bias=bias)
+    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"dominant key bias {name}")
