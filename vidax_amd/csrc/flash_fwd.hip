@@ -179,27 +179,39 @@ void flash_fwd_kernel(const FlashArgs a) {
     klane[p] = (uint32_t)(r * (int)a.ks[1] + col_el) * 2u;
     vlane[p] = (uint32_t)(r * (int)a.vs[1] + col_el) * 2u;
   }
-  // copy p of this wave for tile t
-  auto stage_one = [&](const bf16* base, const LaneSrc (&lanep)[kLoadsPerWave], int64_t sstride, int t, int buf_off,
-                       int p) {
-    if (wave >= kCopyWaves) return;
-    const int i = wave * kLoadsPerWave + p;
-    const i32x4_rsrc rs = raw_rsrc(base + (int64_t)(t * kBN) * sstride);
-    uint32_t voff;
+  // Byte address of this head's first k / v row and the byte distance
+  // between consecutive 64-key tiles, in scalar registers: each tile's copies
+  // go through one buffer resource based at the tile's first row, formed with
+  // scalar adds.
+  const uint64_t k_addr = uniform_u64((uint64_t)(uintptr_t)kg);
+  const uint64_t v_addr = uniform_u64((uint64_t)(uintptr_t)vg);
+  const uint64_t k_tile_bytes = uniform_u64((uint64_t)a.ks[1] * (2 * kBN));
+  const uint64_t v_tile_bytes = uniform_u64((uint64_t)a.vs[1] * (2 * kBN));
+  // this wave's copies of tile t into the LDS tile at buf_off: a whole tile
+  // (every row below kv_end) issues its copies back to back with per-lane
+  // offsets computed once; only the tail tile clamps its rows (one uniform
+  // branch per tile and tensor)
+  auto stage = [&](uint64_t addr0, uint64_t tile_bytes, const LaneSrc (&lanep)[kLoadsPerWave], int64_t sstride,
+                   int t, int buf_off) {
+    const i32x4_rsrc rs = raw_rsrc_u64(addr0 + (uint64_t)t * tile_bytes);
+    const uint32_t dst = lds_base + buf_off + (uint32_t)(wave * kLoadsPerWave) * 1024u;
     if ((t + 1) * kBN <= kv_end) {
-      voff = lanep[p];
+#pragma unroll
+      for (int p = 0; p < kLoadsPerWave; ++p) lds_dma16_buf(rs, lanep[p], dst + p * 1024);
     } else {
       // tail tile: rows past kv_end repeat row kv_end - 1
-      const int r = 8 * (i & 7) + srow;
-      const int rr = min(r, kv_end - 1 - t * kBN);
-      voff = (uint32_t)(rr * (int)sstride + (i >> 3) * 64 + ((scol ^ half_swizzle(r)) * 8)) * 2u;
-    }
-    lds_dma16_buf(rs, voff, lds_base + buf_off + i * 1024);
-  };
-  auto stage = [&](const bf16* base, const LaneSrc (&lanep)[kLoadsPerWave], int64_t sstride, int t, int buf_off) {
 #pragma unroll
-    for (int p = 0; p < kLoadsPerWave; ++p) stage_one(base, lanep, sstride, t, buf_off, p);
+      for (int p = 0; p < kLoadsPerWave; ++p) {
+        const int i = wave * kLoadsPerWave + p;
+        const int r = 8 * (i & 7) + srow;
+        const int rr = min(r, kv_end - 1 - t * kBN);
+        const uint32_t voff = (uint32_t)(rr * (int)sstride + (i >> 3) * 64 + ((scol ^ half_swizzle(r)) * 8)) * 2u;
+        lds_dma16_buf(rs, voff, dst + p * 1024);
+      }
+    }
   };
+  auto stage_k = [&](int t, int buf_off) { stage(k_addr, k_tile_bytes, klane, a.ks[1], t, buf_off); };
+  auto stage_v = [&](int t, int buf_off) { stage(v_addr, v_tile_bytes, vlane, a.vs[1], t, buf_off); };
 
   // A per-key bias enters the scores through the QK^T accumulator: it starts
   // at bias / scale for the lane's keys kb*32 + g*8 + hf*4 + 0..3 of tile j
@@ -311,9 +323,9 @@ void flash_fwd_kernel(const FlashArgs a) {
     // that every wait below counts whole groups.
 #pragma unroll
     for (int j = 0; j < kNB; ++j) {
-      stage(kg, klane, a.ks[1], min(j, n_tiles - 1), kKBuf + j * kTileBytes);
+      if (wave < kCopyWaves) stage_k(min(j, n_tiles - 1), kKBuf + j * kTileBytes);
       stage_mask(min(j, n_tiles - 1));
-      if (j >= 2) stage(vg, vlane, a.vs[1], min(j - 2, n_tiles - 1), kVBuf + (j - 2) * kTileBytes);
+      if (j >= 2 && wave < kCopyWaves) stage_v(min(j - 2, n_tiles - 1), kVBuf + (j - 2) * kTileBytes);
     }
 #pragma unroll
     for (int p = 0; p < kTileBytes / (kThreads * 16); ++p)
@@ -343,8 +355,12 @@ void flash_fwd_kernel(const FlashArgs a) {
     // tile t-1), produces Sn (scores of tile t+1) and P (probabilities of
     // tile t). The loop below calls it twice per trip with the two register
     // sets swapped, so no copies are needed between tiles.
-    auto step = [&](const int t, f32x16 (&S)[2], f32x16 (&Sn)[2], const bf16x8 (&Pp)[2][2],
-                    bf16x8 (&P)[2][2]) {
+    // COPY (a compile-time tag): this wave issues tile copies. The 8-wave
+    // workgroups run two copies of the loop, one for the copying waves and
+    // one for the others, so that neither carries the other's branches.
+    auto step = [&](auto copy_tag, const int t, f32x16 (&S)[2], f32x16 (&Sn)[2], const bf16x8 (&Pp)[2][2],
+                    bf16x8 (&P)[2][2]) __attribute__((always_inline)) {
+      constexpr bool COPY = decltype(copy_tag)::value;
       // K_{t+1} and V_{t-1} have landed once wait_prev returns; the barrier
       // then publishes them, and it also frees K buffer t % kNB (K_t, read by
       // QK(t) last iteration) and V buffer (t+kNB-2) % kNB (V_{t-2}) for this
@@ -367,9 +383,11 @@ void flash_fwd_kernel(const FlashArgs a) {
       }
       if (MASK & kMaskFull) slow = true;
       // this iteration's copies: K_{t+kNB}, its mask and V_{t+kNB-2}
-      stage(kg, klane, a.ks[1], min(t + kNB, n_tiles - 1), kKBuf + kb_next * kTileBytes);
-      stage_mask(min(t + kNB, n_tiles - 1));
-      stage(vg, vlane, a.vs[1], min(t + kNB - 2, n_tiles - 1), kVBuf + vb_next * kTileBytes);
+      if (COPY) {
+        stage_k(min(t + kNB, n_tiles - 1), kKBuf + kb_next * kTileBytes);
+        stage_mask(min(t + kNB, n_tiles - 1));
+        stage_v(min(t + kNB - 2, n_tiles - 1), kVBuf + vb_next * kTileBytes);
+      }
       float cc = c;
       if (slow) {
         cc = 1.0f;
@@ -434,7 +452,7 @@ void flash_fwd_kernel(const FlashArgs a) {
         // CU) for every wave, ahead of the other workgroup's wave while that
         // one copies, waits or starts (+2-4 % at 512 keys).
         constexpr bool kAllPrio = WAVES == 4;
-        if (kAllPrio || wave >= kCopyWaves) __builtin_amdgcn_s_setprio(1);
+        if (kAllPrio || !COPY) __builtin_amdgcn_s_setprio(1);
         bf16x8 fr[kSlots];
         float pf[32];
         bf16x2 pk[16];
@@ -460,7 +478,7 @@ void flash_fwd_kernel(const FlashArgs a) {
           for (int i = 0; i < 16; ++i) l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[i], one2, l_tile, false);
           __builtin_amdgcn_sched_barrier(0);
         };
-        if (WAVES == 4) softmax_block();
+        if (WAVES == 4 || COPY) softmax_block();
         acc_init(t + 1, Sn);  // read by the QK^T slots (16 and on)
 #pragma unroll
         for (int s = 0; s < kSlots; ++s) {
@@ -474,9 +492,9 @@ void flash_fwd_kernel(const FlashArgs a) {
           }
           __builtin_amdgcn_sched_barrier(0);
         }
-        if (WAVES == 4 || wave >= kCopyWaves) __builtin_amdgcn_s_setprio(0);
+        if (kAllPrio || !COPY) __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
-        if (WAVES == 8) softmax_block();
+        if (WAVES == 8 && !COPY) softmax_block();
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -511,18 +529,24 @@ void flash_fwd_kernel(const FlashArgs a) {
 
     f32x16 S2[2];
     bf16x8 P2[2][2];
-    int t = 0;
-    for (; t + 1 < n_tiles; t += 2) {
-      step(t, S, S2, Pp, P2);
-      step(t + 1, S2, S, P2, Pp);
-    }
-    if (t < n_tiles) {
-      step(t, S, S2, Pp, P2);
+    auto key_loop = [&](auto copy_tag) __attribute__((always_inline)) {
+      int t = 0;
+      for (; t + 1 < n_tiles; t += 2) {
+        step(copy_tag, t, S, S2, Pp, P2);
+        step(copy_tag, t + 1, S2, S, P2, Pp);
+      }
+      if (t < n_tiles) {
+        step(copy_tag, t, S, S2, Pp, P2);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) Pp[kb][j] = P2[kb][j];
-    }
+          for (int j = 0; j < 2; ++j) Pp[kb][j] = P2[kb][j];
+      }
+    };
+    if (kCopyWaves == kWaves || wave < kCopyWaves)
+      key_loop(std::integral_constant<bool, true>{});
+    else
+      key_loop(std::integral_constant<bool, kCopyWaves == kWaves>{});
     // ---- PV of the last tile (V_{n-1} sits in V buffer vb_prev now).
     wait_vmem<0>();
     __syncthreads();

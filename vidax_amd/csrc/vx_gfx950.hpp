@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace vx {
 
 typedef __bf16 bf16;
@@ -149,6 +151,24 @@ __device__ __forceinline__ i32x4_rsrc raw_rsrc(const void* base) {
   return r;
 }
 
+// A wave-uniform 64-bit value moved to scalar registers, so that address
+// arithmetic on it stays on the scalar unit.
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((int)(uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((int)(uint32_t)(x >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// raw_rsrc from a wave-uniform byte address.
+__device__ __forceinline__ i32x4_rsrc raw_rsrc_u64(uint64_t addr) {
+  i32x4_rsrc r;
+  r[0] = (int)(uint32_t)addr;
+  r[1] = (int)(uint32_t)(addr >> 32);
+  r[2] = -1;
+  r[3] = 0x00020000;
+  return r;
+}
+
 // The same copy from a buffer resource: lane L fetches 16 bytes at byte
 // offset voff. A 32-bit offset per lane (not a 64-bit address) makes the
 // instruction cheaper to issue.
@@ -156,6 +176,14 @@ __device__ __forceinline__ void lds_dma16_buf(i32x4_rsrc rsrc, uint32_t voff, ui
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :
                : "v"(voff), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(lds_row))
+               : "memory", "m0");
+}
+
+// lds_dma16_buf with a scalar byte offset added to every lane's offset.
+__device__ __forceinline__ void lds_dma16_buf_so(i32x4_rsrc rsrc, uint32_t voff, uint32_t soff, uint32_t lds_row) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(soff), "s"(__builtin_amdgcn_readfirstlane(lds_row))
                : "memory", "m0");
 }
 
