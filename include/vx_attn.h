@@ -26,7 +26,7 @@ extern "C" {
 #define VX_ERR_UNSUPPORTED 2      /* a valid request this build has no kernel for   */
 #define VX_ERR_LAUNCH 3           /* the HIP runtime refused the launch             */
 
-/* Version of this ABI (major * 10000 + minor * 100 + patch). */
+/* Version of this ABI (major * 10000 + minor * 100 + patch): 1.5.0. */
 int32_t vx_abi_version(void);
 
 /* Message describing the most recent failure on the calling thread ("" if none). */
@@ -219,6 +219,44 @@ int32_t vx_rmsnorm_scale_rope_check(const void* x, const void* out, const float*
                                     const float* rope_sin, int64_t rope_stride, int32_t batch, int32_t seq,
                                     int32_t num_heads, int32_t head_dim, const int64_t* x_strides,
                                     const int64_t* out_strides);
+
+/*
+ * Launch plan of vx_flash_attn_fwd / vx_flash_attn_bias_fwd for a shape (host
+ * only, no GPU): writes the name of the kernel those calls would launch,
+ * "flash_fwd_kernel<mask_kind, head_dim, waves>", into kernel_name
+ * (name_len bytes, NUL-terminated). mask_kind is a bit set: 1 key_valid,
+ * 2 key_bias, 4 a per-(query, key) bias. waves is 8 (256-query workgroups)
+ * for long key sequences on large grids, else 4 (128-query workgroups), per
+ * the library's gfx950 tile table; the environment variable
+ * VIDAX_FLASH_BLOCK_SIZES="block_q,block_k_major,block_k" (block_q 128 or
+ * 256, key tiles 64) or "default" overrides it. The variable is read once,
+ * at the first flash call or plan of the process; a malformed value makes
+ * every flash call and plan fail with VX_ERR_INVALID_ARGUMENT, an
+ * unsupported one with VX_ERR_UNSUPPORTED.
+ *
+ * Replaces the reference's tile-size selection:
+ *   - src/vidax/core/attention.py:10-35 (_FLASH_BLOCK_SIZES_BY_DEVICE_KIND,
+ *     _flash_block_sizes and its VIDAX_FLASH_BLOCK_SIZES override)
+ */
+int32_t vx_flash_attn_plan(int32_t batch, int32_t seq_q, int32_t seq_k, int32_t num_heads, int32_t head_dim,
+                           int32_t mask_kind, char* kernel_name, int32_t name_len);
+
+/*
+ * Launch plan of vx_na3d_fwd (host only): the name of the kernel chosen by
+ * the clamped x window, e.g. "na3d_pipe_kernel<16, 128>", written as by
+ * vx_flash_attn_plan. Fails as vx_na3d_check would for the same sizes.
+ * Part of the replacement of src/vidax/models/ltx2_5/diffusion_vae.py:179-234.
+ */
+int32_t vx_na3d_plan(int32_t t, int32_t h, int32_t w, int32_t head_dim, int32_t kernel_t, int32_t kernel_h,
+                     int32_t kernel_w, char* kernel_name, int32_t name_len);
+
+/*
+ * Name of the kernel launched by the last successful vx_*_fwd call on the
+ * calling thread ("" before the first), recorded by the launcher from the
+ * launched instantiation. For tests and profiling: it observes the launch
+ * itself rather than a copy of the launch rule.
+ */
+const char* vx_last_launch(void);
 
 /*
  * Failure injection for error-path tests: while `code` is non-zero, every

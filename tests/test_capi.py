@@ -32,7 +32,7 @@ def test_header_symbols_are_exported():
 
 
 def test_abi_version():
-    assert _lib.lib().vx_abi_version() == 10400
+    assert _lib.lib().vx_abi_version() == 10500
 
 
 def _flash_check(**kw):
@@ -72,6 +72,8 @@ def test_flash_check_accepts_valid_arguments():
     (dict(key_valid=A, stride=258), _lib.VX_ERR_INVALID_ARGUMENT, "key_mask_stride"),
     (dict(key_valid=A + 2, stride=256), _lib.VX_ERR_INVALID_ARGUMENT, "4-byte"),
     (dict(key_bias=A + 4, stride=256), _lib.VX_ERR_INVALID_ARGUMENT, "16-byte"),
+    # a key bias enters the accumulator as bias / scale: 1 / scale must be finite
+    (dict(key_bias=A, stride=256, scale=1e-39), _lib.VX_ERR_INVALID_ARGUMENT, "too small"),
 ])
 def test_flash_check_rejects(kw, code, frag):
     assert _flash_check(**kw) == code
@@ -248,8 +250,9 @@ def test_flash_bias_check():
 
 
 def test_flash_kernel_name_follows_the_launch_rule():
-    """The profiling name mirrors the launcher: 128-query workgroups for key
-    sequences up to 1024 or fewer than 768 256-query tiles, else 256-query."""
+    """The C ABI's launch plan (gfx950 tile table): 128-query workgroups for
+    key sequences up to 1024 or fewer than 768 256-query tiles, else 256-query.
+    (The GPU tests check that the launch itself matches the plan.)"""
     from vidax_amd.attention import flash_kernel_name
     assert flash_kernel_name(1, 32760, 32760, 40) == "flash_fwd_kernel<0, 128, 8>"
     assert flash_kernel_name(1, 119056, 119056, 24, 128, 1) == "flash_fwd_kernel<1, 128, 8>"
@@ -275,7 +278,7 @@ def test_kv_views_with_oversized_sequence_stride_are_copied():
 
 
 def test_na3d_kernel_name_follows_the_launch_rule():
-    """The profiling-name helper mirrors the launcher's choice by the clamped x window."""
+    """The C ABI's NA launch plan, by the clamped x window."""
     from vidax_amd.natten import na3d_kernel_name
     assert na3d_kernel_name(80, 7) == "na3d_pipe_kernel<16, 128>"
     assert na3d_kernel_name(80, 9, 64) == "na3d_pipe_kernel<16, 64>"
@@ -285,3 +288,112 @@ def test_na3d_kernel_name_follows_the_launch_rule():
     assert na3d_kernel_name(80, 14) == "na3d_pipe_kernel<32, 128>"
     assert na3d_kernel_name(80, 25, 64) == "na3d_pipe_kernel<32, 64>"
     assert na3d_kernel_name(80, 27) == "na3d_wave_kernel"
+
+
+def test_small_scale_without_key_bias_is_accepted():
+    assert _flash_check(scale=1e-39) == _lib.VX_OK
+
+
+def _plan_in_subprocess(env_value, code):
+    """Runs `code` in a fresh interpreter with VIDAX_FLASH_BLOCK_SIZES set
+    (the library reads it once per process) and returns its stdout."""
+    import subprocess
+    import sys
+    env = dict(os.environ)
+    if env_value is None:
+        env.pop("VIDAX_FLASH_BLOCK_SIZES", None)
+    else:
+        env["VIDAX_FLASH_BLOCK_SIZES"] = env_value
+    res = subprocess.run([sys.executable, "-c", "import sys; sys.path.insert(0, %r)\n" % ROOT + code],
+                         env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=120)
+    assert res.returncode == 0, res.stdout
+    return res.stdout.strip().splitlines()[-1]
+
+
+_PLANS = ("from vidax_amd import _lib\n"
+          "import ctypes\n"
+          "b = ctypes.create_string_buffer(64)\n"
+          "out = []\n"
+          "for shape in [(1, 32760, 32760, 40), (2, 32760, 512, 40), (1, 7800, 7800, 12)]:\n"
+          "    rc = _lib.lib().vx_flash_attn_plan(*shape, 128, 0, b, 64)\n"
+          "    out.append(b.value.decode() if rc == 0 else 'rc=%d:%s' % (rc, _lib.last_error()))\n"
+          "print('|'.join(out))\n")
+
+
+@pytest.mark.parametrize("value,expect", [
+    (None, ["flash_fwd_kernel<0, 128, 8>", "flash_fwd_kernel<0, 128, 4>", "flash_fwd_kernel<0, 128, 4>"]),
+    ("default", ["flash_fwd_kernel<0, 128, 8>", "flash_fwd_kernel<0, 128, 4>", "flash_fwd_kernel<0, 128, 4>"]),
+    (" DEFAULT ", ["flash_fwd_kernel<0, 128, 8>", "flash_fwd_kernel<0, 128, 4>", "flash_fwd_kernel<0, 128, 4>"]),
+    ("128,64,64", ["flash_fwd_kernel<0, 128, 4>"] * 3),
+    ("256, 64, 64", ["flash_fwd_kernel<0, 128, 8>"] * 3),
+])
+def test_flash_block_sizes_override(value, expect):
+    """VIDAX_FLASH_BLOCK_SIZES (the reference's override, core/attention.py:
+    17-35) picks the query tile for every call; "default" keeps the table."""
+    assert _plan_in_subprocess(value, _PLANS).split("|") == expect
+
+
+@pytest.mark.parametrize("value,code,frag", [
+    ("2048,1024,1024", _lib.VX_ERR_UNSUPPORTED, "key tiles of 64"),
+    ("192,64,64", _lib.VX_ERR_UNSUPPORTED, "query tiles of 128 or 256"),
+    ("256,64", _lib.VX_ERR_INVALID_ARGUMENT, "block_q,block_k_major,block_k"),
+    ("256,64,64,1", _lib.VX_ERR_INVALID_ARGUMENT, "block_q,block_k_major,block_k"),
+    ("big", _lib.VX_ERR_INVALID_ARGUMENT, "block_q,block_k_major,block_k"),
+])
+def test_flash_block_sizes_override_rejects(value, code, frag):
+    """A malformed or unsupported override fails every flash plan and call
+    (here through vx_flash_attn_check) with a message naming the variable."""
+    code_str = ("from vidax_amd import _lib\n"
+                "import ctypes\n"
+                "b = ctypes.create_string_buffer(64)\n"
+                "rc1 = _lib.lib().vx_flash_attn_plan(1, 100, 100, 2, 128, 0, b, 64)\n"
+                "e1 = _lib.last_error()\n"
+                "A = 1 << 20\n"
+                "rc2 = _lib.lib().vx_flash_attn_check(A, A, A, A, None, None, None, 0, 1, 100, 100, 2, 128,"
+                " None, None, None, None, ctypes.c_float(0.1))\n"
+                "print('%d|%d|%s' % (rc1, rc2, e1))\n")
+    rc1, rc2, msg = _plan_in_subprocess(value, code_str).split("|", 2)
+    assert int(rc1) == code and int(rc2) == code
+    assert frag in msg and "VIDAX_FLASH_BLOCK_SIZES" in msg
+
+
+def test_last_launch_is_empty_before_any_launch():
+    out = _plan_in_subprocess(None, "from vidax_amd import _lib\nprint(repr(_lib.last_launch()))\n")
+    assert out == "''"
+
+
+def test_full_bias_broadcasts_every_unit_dim():
+    """Biases broadcast as jnp.broadcast_to does (core/attention.py:282,533):
+    any dim of size 1, including the key dim, which is expanded."""
+    import torch
+    from vidax_amd.attention import _full_bias, _key_only
+    B, H, Sq, Sk = 2, 3, 5, 70
+    for shape in [(1, H, Sq, 1), (B, 1, Sq, 1), (B, H, Sq, Sk), (H, Sq, Sk), (Sq, 1), (1, 1, 1, Sk)]:
+        x = torch.randn(shape)
+        fb, strides = _full_bias(x, B, H, Sq, Sk, "cpu")
+        assert fb.shape[3] == 128 and fb.dtype == torch.float32
+        full = torch.broadcast_to(x.reshape((1,) * (4 - x.dim()) + tuple(shape)), (B, H, Sq, Sk))
+        for b in range(B):
+            for h in range(H):
+                for q in range(Sq):
+                    row = fb.flatten()[b * strides[0] + h * strides[1] + q * strides[2]:][:Sk]
+                    assert torch.equal(row, full[b, h, q]), shape
+    with pytest.raises(ValueError):
+        _full_bias(torch.zeros(1, H, Sq, 7), B, H, Sq, Sk, "cpu")
+    m = torch.tensor([True, False]).reshape(2, 1, 1, 1)
+    assert torch.equal(_key_only(m, B, Sk, "mask"), m.reshape(2, 1).expand(2, Sk))
+    assert _key_only(torch.zeros(1, 1, Sq, 1), B, Sk, "bias") is None
+
+
+def test_na3d_inputs_are_realigned():
+    """A contiguous view at an address that is not 16-byte aligned is copied
+    for the kernel; aligned contiguous tensors are passed as they are."""
+    import torch
+    from vidax_amd.natten import _aligned16
+    buf = torch.zeros(4096, dtype=torch.bfloat16)
+    view = buf[3:3 + 2 * 4 * 8].view(1, 1, 1, 2, 4, 8)
+    assert view.data_ptr() % 16 != 0
+    fixed = _aligned16(view)
+    assert fixed.data_ptr() % 16 == 0 and torch.equal(fixed, view)
+    good = buf[8:8 + 64].view(1, 1, 1, 2, 4, 8)
+    assert _aligned16(good) is good

@@ -183,6 +183,18 @@ def test_flash_config1_full(gpu):
     _check(out, ref, "c1")
 
 
+def _residue_rows(n_total, per_residue, seed):
+    """Query rows covering every position of a 256-query workgroup tile
+    (every residue mod 256: all 8 waves x 32 query lanes) `per_residue` times,
+    in tiles spread over the sequence, plus the first and last rows."""
+    rng = np.random.default_rng(seed)
+    rows = {0, n_total - 1}
+    for r in range(256):
+        tiles = np.arange((n_total - 1 - r) // 256 + 1)
+        rows.update(int(r + 256 * t) for t in rng.choice(tiles, size=min(per_residue, len(tiles)), replace=False))
+    return np.array(sorted(rows))
+
+
 def _rows(n_total, n, seed):
     rng = np.random.default_rng(seed)
     rows = rng.choice(n_total, size=n, replace=False)
@@ -205,12 +217,15 @@ def _np(t):
 
 @pytest.mark.slow
 def test_flash_config2_sampled_rows(gpu):
-    """Headline shape B=1 H=40 L=32760: 160 sampled query rows (all heads) vs the oracle."""
-    from vidax_amd import flash_attention
+    """Headline shape B=1 H=40 L=32760: 514 sampled query rows (all heads)
+    vs the oracle, two per position of a 256-query workgroup tile."""
+    from vidax_amd import _lib, flash_attention
     _say("flash c2 B=1 H=40 L=32760 sampled rows")
     q, k, v = _torch_inputs(1, 32760, 32760, 40, 1, gpu)
     out = flash_attention(q, k, v)
-    rows = _rows(32760, 160, 1)
+    assert _lib.last_launch() == "flash_fwd_kernel<0, 128, 8>", _lib.last_launch()
+    rows = _residue_rows(32760, 2, 1)
+    assert len(rows) >= 512
     ref = O.attention_rows(_np(q), _np(k), _np(v), rows)
     _check(out[:, torch.from_numpy(rows).to(gpu)], ref, "c2 rows")
 
@@ -235,7 +250,8 @@ def test_flash_config3_cross_kvlen(gpu):
 
 @pytest.mark.slow
 def test_flash_config5_joint_sampled_rows(gpu):
-    """Joint text+video B=1 H=24, S = 33*45*80 + 256 = 119056, last p ~ U{0..200} keys invalid."""
+    """Joint text+video B=1 H=24, S = 33*45*80 + 256 = 119056, last p ~ U{0..200}
+    keys invalid; 514 sampled query rows, two per position of a 256-query tile."""
     from vidax_amd import masked_self_attention
     _say("flash c5 joint B=1 H=24 S=119056 key padding")
     S = 33 * 45 * 80 + 256
@@ -245,7 +261,10 @@ def test_flash_config5_joint_sampled_rows(gpu):
     if p:
         valid[:, S - p:] = False
     out = masked_self_attention(q, k, v, key_valid=valid).reshape(1, S, 24, 128)
-    rows = _rows(S, 48, 4)
+    from vidax_amd import _lib
+    assert _lib.last_launch() == "flash_fwd_kernel<1, 128, 8>", _lib.last_launch()
+    rows = _residue_rows(S, 2, 4)
+    assert len(rows) >= 512
     ref = O.attention_rows(_np(q), _np(k), _np(v), rows, key_valid=_np(valid).astype(bool))
     _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"c5 rows (p={p})")
 
@@ -368,12 +387,10 @@ EIGHT_WAVE_KINDS = ["plain", "kv_len", "key_valid", "key_bias", "all_key_masks",
 @pytest.mark.parametrize("D", [128, 64])
 @pytest.mark.parametrize("kind", EIGHT_WAVE_KINDS)
 def test_flash_eight_wave_variants(gpu, D, kind):
-    from vidax_amd import dot_product_attention, flash_attention
-    from vidax_amd.attention import flash_kernel_name
+    from vidax_amd import _lib, dot_product_attention, flash_attention
     B, Sq, Sk, H = 1, 8192, 1100, 24
     mask_kind = {"plain": 0, "kv_len": 0, "key_valid": 1, "key_bias": 2, "all_key_masks": 3, "full_bias": 5}[kind]
-    name = flash_kernel_name(B, Sq, Sk, H, D, mask_kind)
-    assert name.endswith(", 8>"), name
+    name = f"flash_fwd_kernel<{mask_kind}, {D}, 8>"
     _say(f"flash 8 waves {name} kind={kind} B={B} Sq={Sq} Sk={Sk} H={H} D={D}")
     seed = 90 + EIGHT_WAVE_KINDS.index(kind) + (0 if D == 128 else 10)
     q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, D, seed)
@@ -406,6 +423,7 @@ def test_flash_eight_wave_variants(gpu, D, kind):
         bias = (0.5 * rng.standard_normal((B, 1, Sq, Sk))).astype(np.float32)
         out = dot_product_attention(tq, tk, tv, bias=dev(bias), mask=dev(valid[:, None, None, :]))
         ref = O.attention(q[:, rows], k, v, key_valid=valid, bias=bias[:, :, rows])
+    assert _lib.last_launch() == name, _lib.last_launch()  # the kernel that actually ran
     torch.cuda.synchronize()
     _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"8 waves {kind} D={D}")
 
@@ -415,11 +433,9 @@ def test_flash_eight_wave_two_batch_items(gpu, D):
     """8-wave kernel with B=2: per-item kv_len (one inside a tile, one
     below Sk by a whole tile and more) and key_valid holes, sampled rows of
     both items."""
-    from vidax_amd import flash_attention
-    from vidax_amd.attention import flash_kernel_name
+    from vidax_amd import _lib, flash_attention
     B, Sq, Sk, H = 2, 4096, 1100, 24
-    name = flash_kernel_name(B, Sq, Sk, H, D, 1)
-    assert name.endswith(", 8>"), name
+    name = f"flash_fwd_kernel<1, {D}, 8>"
     _say(f"flash 8 waves B=2 {name} Sq={Sq} Sk={Sk} H={H} D={D}")
     seed = 120 + (0 if D == 128 else 1)
     q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, D, seed)
@@ -430,6 +446,7 @@ def test_flash_eight_wave_two_batch_items(gpu, D):
     rows = _rows(Sq, 160, seed)
     dev = lambda a: torch.from_numpy(a).to(gpu)
     out = flash_attention(_t(q, gpu), _t(k, gpu), _t(v, gpu), kv_len=dev(kv_len), key_valid=dev(valid))
+    assert _lib.last_launch() == name, _lib.last_launch()
     torch.cuda.synchronize()
     ref = O.attention(q[:, rows], k, v, kv_len=kv_len, key_valid=valid)
     _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"8 waves B=2 D={D}")
@@ -442,10 +459,9 @@ def test_flash_dominant_key_bias(gpu, shape, D):
     of the sequence as in Cosmos3's text padding) with a small scale (0.02):
     the bias enters the QK^T accumulator as bias / scale (up to 2000), and
     the reference point has to follow the bias, not q.k."""
-    from vidax_amd import flash_attention
-    from vidax_amd.attention import flash_kernel_name
+    from vidax_amd import _lib, flash_attention
     B, Sq, Sk, H = shape
-    name = flash_kernel_name(B, Sq, Sk, H, D, 2)
+    name = f"flash_fwd_kernel<2, {D}, {4 if Sq < 1000 else 8}>"
     _say(f"flash dominant key bias {name} B={B} Sq={Sq} Sk={Sk} H={H} D={D}")
     seed = 130 + (0 if D == 128 else 1) + (0 if Sq < 1000 else 2)
     q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, D, seed)
@@ -456,6 +472,84 @@ def test_flash_dominant_key_bias(gpu, shape, D):
     rows = _rows(Sq, min(Sq, 160), seed)
     out = flash_attention(_t(q, gpu), _t(k, gpu), _t(v, gpu), scale=0.02,
                           key_bias=torch.from_numpy(bias).to(gpu))
+    assert _lib.last_launch() == name, _lib.last_launch()
     torch.cuda.synchronize()
     ref = O.attention(q[:, rows], k, v, scale=0.02, key_bias=bias)
     _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"dominant key bias {name}")
+
+
+# ----------------------------------------- key-axis broadcast of bias / mask
+def test_flash_bias_and_mask_broadcast_along_keys(gpu):
+    """A (1, H, Sq, 1) bias and a (B, 1, Sq, 1) boolean mask broadcast over the
+    keys as jnp.broadcast_to does (src/vidax/core/attention.py:282,533): a
+    per-(head, query) constant bias leaves the softmax unchanged, and a
+    per-(batch, query) False masks every key of that query row."""
+    from vidax_amd import dot_product_attention
+    _say("flash bias (1,H,Sq,1) and mask (B,1,Sq,1)")
+    B, Sq, Sk, H = 2, 90, 300, 3
+    q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, 128, 140)
+    rng = np.random.default_rng(141)
+    tq, tk, tv = _t(q, gpu), _t(k, gpu), _t(v, gpu)
+    bias = (3.0 * rng.standard_normal((1, H, Sq, 1))).astype(np.float32)
+    out = dot_product_attention(tq, tk, tv, bias=torch.from_numpy(bias).to(gpu))
+    torch.cuda.synchronize()
+    _check(out, O.attention(q, k, v, bias=bias), "bias (1,H,Sq,1)")
+    _check(out, O.attention(q, k, v), "bias (1,H,Sq,1) = no bias")
+    mask = np.ones((B, 1, Sq, 1), bool)
+    mask[0, 0, 10:20, 0] = False
+    mask[1, 0, 50, 0] = False
+    out = dot_product_attention(tq, tk, tv, mask=torch.from_numpy(mask).to(gpu))
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    keep = np.broadcast_to(mask[:, 0, :, 0][:, :, None, None], o.shape)
+    # rows with every key masked are written as zeros (see INTEGRATION.md)
+    assert (o[~keep] == 0).all()
+    ref = O.attention(q, k, v)
+    err = np.abs(o - ref)[keep]
+    assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS
+
+
+# ------------------------------------------- forced tile sizes (env override)
+_FORCED = """
+import sys, json
+sys.path.insert(0, {root!r})
+import numpy as np, torch
+from oracle import attention_oracle as O
+from vidax_amd import _lib, flash_attention
+B, Sq, Sk, H, D, seed = {shape}
+q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, D, seed)
+rows = np.unique(np.linspace(0, Sq - 1, 96).astype(int))
+t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda().to(torch.bfloat16)
+kv_len = np.array([Sk - 37] * B, np.int32)
+out = flash_attention(t(q), t(k), t(v), kv_len=torch.from_numpy(kv_len).cuda())
+name = _lib.last_launch()
+torch.cuda.synchronize()
+ref = O.attention(q[:, rows], k, v, kv_len=kv_len)
+err = np.abs(out[:, torch.from_numpy(rows).cuda()].float().cpu().numpy() - ref)
+print(json.dumps(dict(name=name, max=float(err.max()), mean=float(err.mean()))))
+"""
+
+
+@pytest.mark.parametrize("block_q,shape", [
+    (256, (1, 700, 1500, 4, 128, 150)),    # the table picks 128-query workgroups here
+    (128, (1, 8192, 1100, 24, 128, 151)),  # and 256-query ones here
+    (256, (2, 300, 520, 3, 64, 152)),
+])
+def test_flash_forced_block_sizes(gpu, block_q, shape):
+    """VIDAX_FLASH_BLOCK_SIZES forces the query tile (read once per process,
+    so each case runs in a fresh interpreter); the forced kernel launches and
+    matches the oracle."""
+    import json
+    import os
+    import subprocess
+    import sys
+    _say(f"flash forced VIDAX_FLASH_BLOCK_SIZES={block_q},64,64 shape={shape}")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, VIDAX_FLASH_BLOCK_SIZES=f"{block_q},64,64")
+    res = subprocess.run([sys.executable, "-c", _FORCED.format(root=root, shape=shape)], env=env,
+                         stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=240)
+    assert res.returncode == 0, res.stdout[-2000:]
+    r = json.loads(res.stdout.strip().splitlines()[-1])
+    print(f"  {r}", flush=True)
+    assert r["name"] == f"flash_fwd_kernel<0, {shape[4]}, {block_q // 32}>"
+    assert r["max"] <= MAX_ABS and r["mean"] <= MEAN_ABS

@@ -55,15 +55,34 @@ NA_CASES = [
 ]
 
 
+def _expected_kernel(W, kw, D):
+    """The NA kernel for a clamped x window kw' = min(kw, W), written out
+    here independently of the library's plan."""
+    k = min(kw, W)
+    if k <= 9:
+        return f"na3d_pipe_kernel<16, {D}>"
+    if k <= 13:
+        return f"na3d_tall_kernel<{D}>"
+    if k <= 25:
+        return f"na3d_pipe_kernel<32, {D}>"
+    return "na3d_wave_kernel"
+
+
+def _run(gpu, shape, ks, seed, D):
+    from vidax_amd import _lib, neighborhood_attention_3d
+    B, T, H, W, NH = shape
+    q, k, v = O.make_na3d_inputs(B, T, H, W, NH, D, seed)
+    out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), ks)
+    launched = _lib.last_launch()
+    assert launched == _expected_kernel(W, ks[2], D), launched
+    torch.cuda.synchronize()
+    _check(out.float().cpu().numpy(), O.na3d(q, k, v, ks), f"oracle ({launched})")
+
+
 @pytest.mark.parametrize("shape,ks,seed", NA_CASES)
 def test_na3d_small(gpu, shape, ks, seed):
-    from vidax_amd import neighborhood_attention_3d
-    B, T, H, W, NH = shape
     _say(f"na3d shape={shape} kernel={ks} seed={seed}")
-    q, k, v = O.make_na3d_inputs(B, T, H, W, NH, 128, seed)
-    out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), ks)
-    torch.cuda.synchronize()
-    _check(out.float().cpu().numpy(), O.na3d(q, k, v, ks), "oracle")
+    _run(gpu, shape, ks, seed, 128)
 
 
 NA_D64_CASES = [
@@ -80,13 +99,27 @@ NA_D64_CASES = [
 
 @pytest.mark.parametrize("shape,ks,seed", NA_D64_CASES)
 def test_na3d_head_dim_64(gpu, shape, ks, seed):
-    from vidax_amd import neighborhood_attention_3d
-    B, T, H, W, NH = shape
     _say(f"na3d D=64 shape={shape} kernel={ks} seed={seed}")
-    q, k, v = O.make_na3d_inputs(B, T, H, W, NH, 64, seed)
-    out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), ks)
-    torch.cuda.synchronize()
-    _check(out.float().cpu().numpy(), O.na3d(q, k, v, ks), "oracle")
+    _run(gpu, shape, ks, seed, 64)
+
+
+# With num_heads % 8 == 0 the kernels remap workgroups so that all bricks of
+# a head land on one XCD; these cases run that remap on every pipelined
+# kernel (16- and 32-key segments, tall bricks) with ragged y and x edges.
+NA_NH8_CASES = [
+    # (B, T, H, W, NH), kernel, seed, D
+    ((1, 3, 11, 21, 8), (3, 11, 11), 60, 64),    # tall, stage-5 window family, D=64
+    ((1, 3, 11, 21, 8), (3, 11, 11), 61, 128),   # tall, D=128
+    ((1, 2, 7, 37, 8), (3, 5, 17), 62, 128),     # 32-key segments (kw' = 17)
+    ((1, 2, 6, 45, 8), (1, 3, 25), 63, 64),      # 32-key segments, widest D=64 window
+    ((2, 3, 9, 19, 16), (3, 7, 7), 64, 128),     # 16-key segments, two batch items
+]
+
+
+@pytest.mark.parametrize("shape,ks,seed,D", NA_NH8_CASES)
+def test_na3d_head_remap(gpu, shape, ks, seed, D):
+    _say(f"na3d NH%8==0 shape={shape} kernel={ks} seed={seed} D={D}")
+    _run(gpu, shape, ks, seed, D)
 
 
 @pytest.mark.parametrize("shift", [-1000.0, -120.0, 200.0, 1000.0])
@@ -153,6 +186,8 @@ def test_na3d_config4_sampled_rows(gpu):
     B, T, H, W, NH = 1, 21, 45, 80, 24
     q, k, v = O.make_na3d_inputs(B, T, H, W, NH, 128, 3)
     out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), (3, 7, 7))
+    from vidax_amd import _lib
+    assert _lib.last_launch() == "na3d_pipe_kernel<16, 128>", _lib.last_launch()
     o = out.float().cpu().numpy()
     rows = [(0, 0), (0, 44), (20, 0), (20, 44), (1, 1), (10, 22), (10, 3), (19, 43),
             (5, 40), (15, 2), (2, 21), (18, 30), (11, 44), (9, 0)]

@@ -33,6 +33,9 @@ EXPORTED_SYMBOLS = (
     "vx_flash_attn_bias_check",
     "vx_rmsnorm_scale_rope_fwd",
     "vx_rmsnorm_scale_rope_check",
+    "vx_flash_attn_plan",
+    "vx_na3d_plan",
+    "vx_last_launch",
 )
 
 _lock = threading.Lock()
@@ -101,12 +104,37 @@ def lib() -> ctypes.CDLL:
             h.vx_rmsnorm_scale_rope_check.argtypes = _SCALED_PROLOGUE_ARGS
             h.vx_debug_inject_error.restype = None
             h.vx_debug_inject_error.argtypes = [_i32]
+            h.vx_flash_attn_plan.restype = _i32
+            h.vx_flash_attn_plan.argtypes = [_i32] * 6 + [ctypes.c_char_p, _i32]
+            h.vx_na3d_plan.restype = _i32
+            h.vx_na3d_plan.argtypes = [_i32] * 7 + [ctypes.c_char_p, _i32]
+            h.vx_last_launch.restype = ctypes.c_char_p
+            h.vx_last_launch.argtypes = []
             _lib = h
     return _lib
 
 
 def last_error() -> str:
     return lib().vx_last_error().decode("utf-8", "replace")
+
+
+def last_launch() -> str:
+    """Kernel launched by the last successful vx_*_fwd call on this thread."""
+    return lib().vx_last_launch().decode("utf-8", "replace")
+
+
+def flash_plan(batch: int, seq_q: int, seq_k: int, num_heads: int, head_dim: int, mask_kind: int) -> str:
+    """Kernel vx_flash_attn_fwd would launch for this shape (host-side plan)."""
+    buf = ctypes.create_string_buffer(64)
+    raise_for(lib().vx_flash_attn_plan(batch, seq_q, seq_k, num_heads, head_dim, mask_kind, buf, 64))
+    return buf.value.decode()
+
+
+def na3d_plan(t: int, h: int, w: int, head_dim: int, kernel_t: int, kernel_h: int, kernel_w: int) -> str:
+    """Kernel vx_na3d_fwd would launch for this grid and window (host-side plan)."""
+    buf = ctypes.create_string_buffer(64)
+    raise_for(lib().vx_na3d_plan(t, h, w, head_dim, kernel_t, kernel_h, kernel_w, buf, 64))
+    return buf.value.decode()
 
 
 def raise_for(code: int) -> None:

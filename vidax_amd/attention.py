@@ -80,17 +80,21 @@ def _last_valid_plus_one(valid: torch.Tensor) -> torch.Tensor:
 
 
 def _full_bias(bias, B: int, H: int, Sq: int, Sk: int, dev) -> Tuple[torch.Tensor, Tuple[int, int, int]]:
-    """A (B|1, H|1, Sq|1, Sk) additive bias as the kernel reads it: fp32, keys
-    contiguous, every query row readable for round_up(Sk, 64) keys, 16-byte
-    aligned, strides multiples of 4 (0 for broadcast dims). Copies only when
-    the given tensor does not already have that form."""
+    """A bias broadcastable to (B, H, Sq, Sk) -- every dim 1 or full, as
+    `jnp.broadcast_to` accepts (`src/vidax/core/attention.py:282,533`) -- as
+    the kernel reads it: fp32, keys contiguous, every query row readable for
+    round_up(Sk, 64) keys, 16-byte aligned, strides multiples of 4 (0 for
+    broadcast dims). A key dim of 1 is expanded; copies only when the given
+    tensor does not already have that form."""
     x = torch.as_tensor(bias, device=dev)
     while x.dim() < 4:
         x = x.unsqueeze(0)
-    if x.dim() != 4 or x.shape[-1] != Sk or any(x.shape[i] not in (1, n) for i, n in enumerate((B, H, Sq))):
+    if x.dim() != 4 or any(x.shape[i] not in (1, n) for i, n in enumerate((B, H, Sq, Sk))):
         raise ValueError(f"bias of shape {tuple(bias.shape)} is not broadcastable to (B, H, Sq, Sk) = "
                          f"({B}, {H}, {Sq}, {Sk})")
     x = x.to(torch.float32)
+    if x.shape[3] != Sk:
+        x = x.expand(x.shape[0], x.shape[1], x.shape[2], Sk)
     width = (Sk + 63) // 64 * 64
     ok = (x.stride(3) == 1 and Sk == width and x.data_ptr() % 16 == 0 and
           all(x.stride(i) % 4 == 0 for i in range(3)))
@@ -180,13 +184,10 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
 
 def flash_kernel_name(batch: int, seq_q: int, seq_k: int, num_heads: int, head_dim: int = 128,
                       mask_kind: int = 0) -> str:
-    """Name of the kernel the library launches (profiling aid): 128-query
-    workgroups (4 waves) for key sequences up to 1024 or grids of fewer than
-    768 256-query tiles, 256-query workgroups (8 waves) otherwise. mask_kind:
+    """Name of the kernel the library launches for this shape (the C ABI's
+    launch plan: the gfx950 tile table or VIDAX_FLASH_BLOCK_SIZES). mask_kind:
     1 key validity, 2 key bias, 4 full bias (bits)."""
-    blocks256 = -(-int(seq_q) // 256) * int(num_heads) * int(batch)
-    waves = 4 if int(seq_k) <= 1024 or blocks256 < 768 else 8
-    return f"flash_fwd_kernel<{int(mask_kind)}, {int(head_dim)}, {waves}>"
+    return _lib.flash_plan(int(batch), int(seq_q), int(seq_k), int(num_heads), int(head_dim), int(mask_kind))
 
 
 def _single_device(mesh) -> None:
@@ -205,12 +206,14 @@ def _single_device(mesh) -> None:
 
 def _key_only(x: torch.Tensor, B: int, Sk: int, what: str) -> Optional[torch.Tensor]:
     """Reduces a tensor broadcastable to (B, H, Sq, Sk) to (B, Sk) if it only
-    varies along batch and key; returns None otherwise."""
+    varies along batch and key (a key dim of 1 broadcasts); returns None
+    otherwise."""
     x = torch.as_tensor(x)
     while x.dim() < 4:
         x = x.unsqueeze(0)
-    if x.dim() != 4:
-        raise ValueError(f"{what} must be broadcastable to (B, H, Sq, Sk)")
+    if x.dim() != 4 or x.shape[0] not in (1, B) or x.shape[3] not in (1, Sk):
+        raise ValueError(f"{what} of shape {tuple(x.shape)} is not broadcastable to (B, H, Sq, Sk) with "
+                         f"B={B}, Sk={Sk}")
     if x.shape[1] != 1 or x.shape[2] != 1:
         return None
     return x.expand(B, 1, 1, Sk).reshape(B, Sk)

@@ -33,6 +33,8 @@
 #include "vx_gfx950.hpp"
 #include "vx_kernels.h"
 
+#include <string>
+
 namespace vx {
 namespace {
 
@@ -569,45 +571,50 @@ void flash_fwd_kernel(const FlashArgs a) {
   }
 }
 
-template <int MASK, int WAVES>
-int launch_waves(const FlashArgs& a, hipStream_t stream) {
+// Name of a flash_fwd_kernel instantiation, as the profiler prints it.
+template <int MASK, int D, int WAVES>
+const char* flash_kernel_name() {
+  static const std::string name = "flash_fwd_kernel<" + std::to_string(MASK) + ", " + std::to_string(D) + ", " +
+                                  std::to_string(WAVES) + ">";
+  return name.c_str();
+}
+
+template <int MASK, int WAVES, int D>
+int launch_one(const FlashArgs& a, hipStream_t stream, const char** launched) {
   dim3 grid((a.Sq + WAVES * 32 - 1) / (WAVES * 32), a.H, a.B);
-  if (a.D == 64)
-    hipLaunchKernelGGL((flash_fwd_kernel<MASK, 64, WAVES>), grid, dim3(WAVES * 64), 0, stream, a);
-  else
-    hipLaunchKernelGGL((flash_fwd_kernel<MASK, 128, WAVES>), grid, dim3(WAVES * 64), 0, stream, a);
+  hipLaunchKernelGGL((flash_fwd_kernel<MASK, D, WAVES>), grid, dim3(WAVES * 64), 0, stream, a);
+  *launched = flash_kernel_name<MASK, D, WAVES>();
   return (int)hipGetLastError();
 }
 
-// Short key sequences (few tiles per query tile) and grids that give most
-// CUs fewer than two 256-query workgroups run on 128-query workgroups, two
-// per CU; long sequences on 256-query workgroups.
+// The workgroup size (4 or 8 waves) comes from the launch plan in a.waves.
 template <int MASK>
-int launch(const FlashArgs& a, hipStream_t stream) {
-  const int64_t blocks256 = (int64_t)((a.Sq + 255) / 256) * a.H * a.B;
-  if (a.Sk <= 1024 || blocks256 < 768) return launch_waves<MASK, 4>(a, stream);
-  return launch_waves<MASK, 8>(a, stream);
+int launch(const FlashArgs& a, hipStream_t stream, const char** launched) {
+  if (a.waves == 4)
+    return a.D == 64 ? launch_one<MASK, 4, 64>(a, stream, launched) : launch_one<MASK, 4, 128>(a, stream, launched);
+  return a.D == 64 ? launch_one<MASK, 8, 64>(a, stream, launched) : launch_one<MASK, 8, 128>(a, stream, launched);
 }
 
 }  // namespace
 
-int launch_flash_fwd(const FlashArgs& a, void* stream) {
+int launch_flash_fwd(const FlashArgs& a, void* stream, const char** launched) {
   if (a.D != 128 && a.D != 64) return (int)hipErrorNotSupported;
+  if (a.waves != 4 && a.waves != 8) return (int)hipErrorInvalidValue;
   hipStream_t s = (hipStream_t)stream;
   const int mask = (a.key_valid != nullptr ? kMaskValid : 0) | (a.key_bias != nullptr ? kMaskBias : 0);
   if (a.full_bias != nullptr) {
     switch (mask) {
-      case kMaskValid: return launch<kMaskFull | kMaskValid>(a, s);
-      case kMaskBias: return launch<kMaskFull | kMaskBias>(a, s);
-      case kMaskValid | kMaskBias: return launch<kMaskFull | kMaskValid | kMaskBias>(a, s);
-      default: return launch<kMaskFull>(a, s);
+      case kMaskValid: return launch<kMaskFull | kMaskValid>(a, s, launched);
+      case kMaskBias: return launch<kMaskFull | kMaskBias>(a, s, launched);
+      case kMaskValid | kMaskBias: return launch<kMaskFull | kMaskValid | kMaskBias>(a, s, launched);
+      default: return launch<kMaskFull>(a, s, launched);
     }
   }
   switch (mask) {
-    case kMaskValid: return launch<kMaskValid>(a, s);
-    case kMaskBias: return launch<kMaskBias>(a, s);
-    case kMaskValid | kMaskBias: return launch<kMaskValid | kMaskBias>(a, s);
-    default: return launch<kMaskNone>(a, s);
+    case kMaskValid: return launch<kMaskValid>(a, s, launched);
+    case kMaskBias: return launch<kMaskBias>(a, s, launched);
+    case kMaskValid | kMaskBias: return launch<kMaskValid | kMaskBias>(a, s, launched);
+    default: return launch<kMaskNone>(a, s, launched);
   }
 }
 

@@ -1,7 +1,8 @@
 // 3D neighbourhood attention forward for gfx950 (NATTEN semantics with
 // boundary-clamped windows), bf16 in/out, head dim 128 or 64.
 //
-// Three kernels, chosen by the clamped x window kw' (launch_na3d_fwd):
+// Three kernels, chosen by the clamped x window kw' (the launch plan of the
+// C ABI, Na3dVariant):
 // - na3d_pipe_kernel<SEG, D> (kw' <= 9 or 13 < kw' <= 25): a workgroup of 4
 //   waves owns a 1 (t) x 4 (y) x 32 (x) query brick of one head and streams
 //   the union of its windows, kt' x NY key rows (t', y'), through LDS with
@@ -685,43 +686,56 @@ void na3d_tall_kernel(const Na3dArgs a, int n_yb, int n_xb) {
 
 }  // namespace
 
-int launch_na3d_fwd(const Na3dArgs& a, void* stream) {
+int launch_na3d_fwd(const Na3dArgs& a, void* stream, const char** launched) {
   if (a.D != 128 && a.D != 64) return (int)hipErrorNotSupported;
   hipStream_t st = (hipStream_t)stream;
-  if (a.kw > 9 && a.kw <= 13) {
-    const int n_yb = (a.Hs + 7) / 8;
-    const int n_xb = (a.W + 15) / 16;
-    dim3 grid((unsigned)a.T * n_yb * n_xb, a.NH, a.B);
-    if (a.D == 128)
-      hipLaunchKernelGGL((na3d_tall_kernel<128>), grid, dim3(256), 0, st, a, n_yb, n_xb);
-    else
-      hipLaunchKernelGGL((na3d_tall_kernel<64>), grid, dim3(256), 0, st, a, n_yb, n_xb);
-    return (int)hipGetLastError();
-  }
-  if (a.kw <= 25) {
-    const int n_yb = (a.Hs + 3) / 4;
-    const int n_xb = (a.W + 31) / 32;
-    dim3 grid((unsigned)a.T * n_yb * n_xb, a.NH, a.B);
-    if (a.D == 128) {
-      if (a.kw <= 9)
-        hipLaunchKernelGGL((na3d_pipe_kernel<16, 128>), grid, dim3(256), 0, st, a, n_yb, n_xb);
-      else
-        hipLaunchKernelGGL((na3d_pipe_kernel<32, 128>), grid, dim3(256), 0, st, a, n_yb, n_xb);
-    } else {
-      if (a.kw <= 9)
-        hipLaunchKernelGGL((na3d_pipe_kernel<16, 64>), grid, dim3(256), 0, st, a, n_yb, n_xb);
-      else
-        hipLaunchKernelGGL((na3d_pipe_kernel<32, 64>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+  switch (a.variant) {
+    case kNaTall: {
+      const int n_yb = (a.Hs + 7) / 8;
+      const int n_xb = (a.W + 15) / 16;
+      dim3 grid((unsigned)a.T * n_yb * n_xb, a.NH, a.B);
+      if (a.D == 128) {
+        hipLaunchKernelGGL((na3d_tall_kernel<128>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+        *launched = "na3d_tall_kernel<128>";
+      } else {
+        hipLaunchKernelGGL((na3d_tall_kernel<64>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+        *launched = "na3d_tall_kernel<64>";
+      }
+      return (int)hipGetLastError();
     }
-    return (int)hipGetLastError();
+    case kNaPipe16:
+    case kNaPipe32: {
+      const int n_yb = (a.Hs + 3) / 4;
+      const int n_xb = (a.W + 31) / 32;
+      dim3 grid((unsigned)a.T * n_yb * n_xb, a.NH, a.B);
+      if (a.variant == kNaPipe16 && a.D == 128) {
+        hipLaunchKernelGGL((na3d_pipe_kernel<16, 128>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+        *launched = "na3d_pipe_kernel<16, 128>";
+      } else if (a.D == 128) {
+        hipLaunchKernelGGL((na3d_pipe_kernel<32, 128>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+        *launched = "na3d_pipe_kernel<32, 128>";
+      } else if (a.variant == kNaPipe16) {
+        hipLaunchKernelGGL((na3d_pipe_kernel<16, 64>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+        *launched = "na3d_pipe_kernel<16, 64>";
+      } else {
+        hipLaunchKernelGGL((na3d_pipe_kernel<32, 64>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+        *launched = "na3d_pipe_kernel<32, 64>";
+      }
+      return (int)hipGetLastError();
+    }
+    case kNaWave: {
+      if (a.D != kD) return (int)hipErrorNotSupported;  // the per-wave kernel is D = 128 only
+      const int n_yb = (a.Hs + kBrickY - 1) / kBrickY;
+      const int n_xb = (a.W + kBrickX - 1) / kBrickX;
+      const int n_xg = (n_xb + kWaves - 1) / kWaves;
+      dim3 grid((unsigned)a.T * n_yb * n_xg, a.NH, a.B);
+      hipLaunchKernelGGL(na3d_wave_kernel, grid, dim3(kWaves * 64), 0, st, a, n_yb, n_xb, n_xg);
+      *launched = "na3d_wave_kernel";
+      return (int)hipGetLastError();
+    }
+    default:
+      return (int)hipErrorInvalidValue;
   }
-  if (a.D != kD) return (int)hipErrorNotSupported;  // the per-wave kernel is D = 128 only
-  const int n_yb = (a.Hs + kBrickY - 1) / kBrickY;
-  const int n_xb = (a.W + kBrickX - 1) / kBrickX;
-  const int n_xg = (n_xb + kWaves - 1) / kWaves;
-  dim3 grid((unsigned)a.T * n_yb * n_xg, a.NH, a.B);
-  hipLaunchKernelGGL(na3d_wave_kernel, grid, dim3(kWaves * 64), 0, st, a, n_yb, n_xb, n_xg);
-  return (int)hipGetLastError();
 }
 
 }  // namespace vx

@@ -21,6 +21,8 @@
 #include "vx_gfx950.hpp"
 #include "vx_kernels.h"
 
+#include <string>
+
 namespace vx {
 namespace {
 
@@ -136,38 +138,48 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const 
   }
 }
 
+template <int NCHUNK, bool FULL>
+const char* prologue_kernel_name() {
+  static const std::string name =
+      "qk_prologue_kernel<" + std::to_string(NCHUNK) + ", " + (FULL ? "true" : "false") + ">";
+  return name.c_str();
+}
+
 template <int NCHUNK>
-int launch(const PrologueArgs& a, hipStream_t st) {
+int launch(const PrologueArgs& a, hipStream_t st, const char** launched) {
   const int64_t rows = (int64_t)a.B * a.S;
   dim3 grid((unsigned)((rows + kWavesPerBlock - 1) / kWavesPerBlock));
-  if ((a.H * a.D) % 512 == 0)
+  if ((a.H * a.D) % 512 == 0) {
     hipLaunchKernelGGL((qk_prologue_kernel<NCHUNK, true>), grid, dim3(kWavesPerBlock * 64), 0, st, a);
-  else
+    *launched = prologue_kernel_name<NCHUNK, true>();
+  } else {
     hipLaunchKernelGGL((qk_prologue_kernel<NCHUNK, false>), grid, dim3(kWavesPerBlock * 64), 0, st, a);
+    *launched = prologue_kernel_name<NCHUNK, false>();
+  }
   return (int)hipGetLastError();
 }
 
 }  // namespace
 
-int launch_qk_prologue(const PrologueArgs& a, void* stream) {
+int launch_qk_prologue(const PrologueArgs& a, void* stream, const char** launched) {
   hipStream_t st = (hipStream_t)stream;
   switch ((a.H * a.D / 8 + 63) / 64) {  // chunks per lane
-    case 1: return launch<1>(a, st);
-    case 2: return launch<2>(a, st);
-    case 3: return launch<3>(a, st);
-    case 4: return launch<4>(a, st);
-    case 5: return launch<5>(a, st);
-    case 6: return launch<6>(a, st);
-    case 7: return launch<7>(a, st);
-    case 8: return launch<8>(a, st);
-    case 9: return launch<9>(a, st);
-    case 10: return launch<10>(a, st);
-    case 11: return launch<11>(a, st);
-    case 12: return launch<12>(a, st);
-    case 13: return launch<13>(a, st);
-    case 14: return launch<14>(a, st);
-    case 15: return launch<15>(a, st);
-    case 16: return launch<16>(a, st);
+    case 1: return launch<1>(a, st, launched);
+    case 2: return launch<2>(a, st, launched);
+    case 3: return launch<3>(a, st, launched);
+    case 4: return launch<4>(a, st, launched);
+    case 5: return launch<5>(a, st, launched);
+    case 6: return launch<6>(a, st, launched);
+    case 7: return launch<7>(a, st, launched);
+    case 8: return launch<8>(a, st, launched);
+    case 9: return launch<9>(a, st, launched);
+    case 10: return launch<10>(a, st, launched);
+    case 11: return launch<11>(a, st, launched);
+    case 12: return launch<12>(a, st, launched);
+    case 13: return launch<13>(a, st, launched);
+    case 14: return launch<14>(a, st, launched);
+    case 15: return launch<15>(a, st, launched);
+    case 16: return launch<16>(a, st, launched);
     default: return (int)hipErrorNotSupported;
   }
 }

@@ -8,7 +8,11 @@
 #include <string.h>
 
 #include <atomic>
+#include <cctype>
 #include <cmath>
+#include <cstdlib>
+#include <mutex>
+#include <string>
 
 #include "../../include/vx_attn.h"
 #include "vx_kernels.h"
@@ -16,6 +20,7 @@
 namespace {
 
 thread_local char g_error[512] = "";
+thread_local const char* g_last_launch = "";
 std::atomic<int32_t> g_inject{0};
 
 int32_t fail(int32_t code, const char* fmt, ...) {
@@ -57,6 +62,111 @@ int32_t check_strides(const char* name, const int64_t s[3], int32_t S) {
   return VX_OK;
 }
 
+// ---- flash launch plan: the gfx950 tile table and its env override.
+//
+// Mirrors the reference's per-device tile table and VIDAX_FLASH_BLOCK_SIZES
+// override (src/vidax/core/attention.py:10-35). Here a tile choice is the
+// query tile of a workgroup: 128 queries (4 waves, two workgroups per CU)
+// or 256 queries (8 waves, one per CU), with 64-key tiles either way. The
+// library holds gfx950 code only, so the table has that one row.
+struct FlashTileRule {
+  const char* arch;
+  int32_t max_seq_k_small;    // key sequences up to this run 128-query workgroups
+  int64_t min_tiles_large;    // grids with fewer 256-query tiles run 128-query workgroups
+};
+constexpr FlashTileRule kFlashTileTable[] = {
+    {"gfx950", 1024, 768},
+};
+constexpr int32_t kKeyTile = 64;
+
+// VIDAX_FLASH_BLOCK_SIZES: "block_q,block_k_major,block_k" or "default"
+// (the table's rule), read once per process.
+struct FlashTileOverride {
+  int32_t block_q = 0;  // 0: no override
+  int32_t rc = VX_OK;   // non-zero: the variable is malformed or unsupported
+  std::string error;
+};
+
+FlashTileOverride parse_tile_override(const char* env) {
+  FlashTileOverride o;
+  if (env == nullptr) return o;
+  std::string v(env);
+  while (!v.empty() && std::isspace((unsigned char)v.back())) v.pop_back();
+  size_t b = 0;
+  while (b < v.size() && std::isspace((unsigned char)v[b])) ++b;
+  v = v.substr(b);
+  if (v.empty()) return o;
+  std::string lower = v;
+  for (auto& ch : lower) ch = (char)std::tolower((unsigned char)ch);
+  if (lower == "default") return o;
+  long vals[3];
+  const char* p = v.c_str();
+  for (int i = 0; i < 3; ++i) {
+    char* end = nullptr;
+    vals[i] = std::strtol(p, &end, 10);
+    while (*end == ' ') ++end;
+    const char want = i < 2 ? ',' : '\0';
+    if (end == p || *end != want) {
+      o.rc = VX_ERR_INVALID_ARGUMENT;
+      o.error = "VIDAX_FLASH_BLOCK_SIZES='" + v + "' must be 'block_q,block_k_major,block_k' or 'default'";
+      return o;
+    }
+    p = end + (i < 2 ? 1 : 0);
+  }
+  if ((vals[0] != 128 && vals[0] != 256) || vals[1] != kKeyTile || vals[2] != kKeyTile) {
+    o.rc = VX_ERR_UNSUPPORTED;
+    o.error = "VIDAX_FLASH_BLOCK_SIZES='" + v +
+              "': this build's flash kernel has query tiles of 128 or 256 and key tiles of 64 "
+              "(e.g. '256,64,64')";
+    return o;
+  }
+  o.block_q = (int32_t)vals[0];
+  return o;
+}
+
+const FlashTileOverride& tile_override() {
+  static std::once_flag once;
+  static FlashTileOverride o;
+  std::call_once(once, [] { o = parse_tile_override(std::getenv("VIDAX_FLASH_BLOCK_SIZES")); });
+  return o;
+}
+
+// Workgroup size for a flash call: the override, else the table's rule.
+int32_t flash_plan(int32_t B, int32_t Sq, int32_t Sk, int32_t H, int32_t* waves) {
+  const FlashTileOverride& o = tile_override();
+  if (o.rc != VX_OK) return fail(o.rc, "%s", o.error.c_str());
+  if (o.block_q != 0) {
+    *waves = o.block_q / 32;
+    return VX_OK;
+  }
+  const FlashTileRule& r = kFlashTileTable[0];
+  const int64_t tiles256 = (int64_t)((Sq + 255) / 256) * H * B;
+  *waves = (Sk <= r.max_seq_k_small || tiles256 < r.min_tiles_large) ? 4 : 8;
+  return VX_OK;
+}
+
+void flash_kernel_label(int32_t mask_kind, int32_t D, int32_t waves, char* out, int32_t len) {
+  if (out != nullptr && len > 0) snprintf(out, (size_t)len, "flash_fwd_kernel<%d, %d, %d>", mask_kind, D, waves);
+}
+
+// ---- neighbourhood-attention launch plan, by the clamped x window.
+int32_t na3d_variant(int32_t kw_clamped, int32_t D) {
+  if (kw_clamped <= 9) return vx::kNaPipe16;
+  if (kw_clamped <= 13) return vx::kNaTall;
+  if (kw_clamped <= 25) return vx::kNaPipe32;
+  (void)D;
+  return vx::kNaWave;
+}
+
+const char* na3d_kernel_label(int32_t variant, int32_t D) {
+  switch (variant) {
+    case vx::kNaPipe16: return D == 64 ? "na3d_pipe_kernel<16, 64>" : "na3d_pipe_kernel<16, 128>";
+    case vx::kNaTall: return D == 64 ? "na3d_tall_kernel<64>" : "na3d_tall_kernel<128>";
+    case vx::kNaPipe32: return D == 64 ? "na3d_pipe_kernel<32, 64>" : "na3d_pipe_kernel<32, 128>";
+    default: return "na3d_wave_kernel";
+  }
+}
+
 int32_t flash_check(const void* q, const void* k, const void* v, const void* out, const int32_t* kv_len,
                     const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride, int32_t B,
                     int32_t Sq, int32_t Sk,
@@ -77,6 +187,10 @@ int32_t flash_check(const void* q, const void* k, const void* v, const void* out
     return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 64 and 128)", D);
   if (!(scale > 0.f) || !std::isfinite(scale))
     return fail(VX_ERR_INVALID_ARGUMENT, "scale must be positive and finite (got %g)", (double)scale);
+  // a key bias enters the kernel's accumulator as bias / scale
+  if (key_bias != nullptr && !std::isfinite(1.0f / scale))
+    return fail(VX_ERR_INVALID_ARGUMENT, "scale %g is too small for a key bias (1/scale is not finite)",
+                (double)scale);
   if (key_valid != nullptr || key_bias != nullptr) {
     const int64_t need = ((int64_t)Sk + 63) / 64 * 64;
     if (key_mask_stride < need || key_mask_stride % 4 != 0)
@@ -110,7 +224,10 @@ int32_t flash_check(const void* q, const void* k, const void* v, const void* out
   if (ks[1] > (int64_t(1) << 24) || vs[1] > (int64_t(1) << 24))
     return fail(VX_ERR_UNSUPPORTED, "k/v sequence strides (%lld, %lld) above 2^24 elements are not supported",
                 (long long)ks[1], (long long)vs[1]);
+  int32_t waves = 0;
+  if ((rc = flash_plan(B, Sq, Sk, H, &waves)) != VX_OK) return rc;
   if (args != nullptr) {
+    args->waves = waves;
     args->q = q;
     args->k = k;
     args->v = v;
@@ -183,6 +300,7 @@ int32_t na3d_check(const void* q, const void* k, const void* v, const void* out,
     args->kh = kh < Hs ? kh : Hs;
     args->kw = kw < W ? kw : W;
     args->scale = scale;
+    args->variant = na3d_variant(args->kw, D);
   }
   return ok();
 }
@@ -259,11 +377,41 @@ int32_t injected() {
 
 extern "C" {
 
-int32_t vx_abi_version(void) { return 10400; }
+int32_t vx_abi_version(void) { return 10500; }
 
 const char* vx_last_error(void) { return g_error; }
 
 void vx_debug_inject_error(int32_t code) { g_inject.store(code, std::memory_order_relaxed); }
+
+const char* vx_last_launch(void) { return g_last_launch; }
+
+int32_t vx_flash_attn_plan(int32_t batch, int32_t seq_q, int32_t seq_k, int32_t num_heads, int32_t head_dim,
+                           int32_t mask_kind, char* kernel_name, int32_t name_len) {
+  if (batch < 1 || seq_q < 1 || seq_k < 1 || num_heads < 1)
+    return fail(VX_ERR_INVALID_ARGUMENT, "batch, seq_q, seq_k and num_heads must be >= 1");
+  if (head_dim != 128 && head_dim != 64)
+    return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 64 and 128)", head_dim);
+  if (mask_kind < 0 || mask_kind > 7) return fail(VX_ERR_INVALID_ARGUMENT, "mask_kind must be in 0..7");
+  int32_t waves = 0;
+  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, &waves);
+  if (rc != VX_OK) return rc;
+  flash_kernel_label(mask_kind, head_dim, waves, kernel_name, name_len);
+  return ok();
+}
+
+int32_t vx_na3d_plan(int32_t t, int32_t h, int32_t w, int32_t head_dim, int32_t kernel_t, int32_t kernel_h,
+                     int32_t kernel_w, char* kernel_name, int32_t name_len) {
+  (void)kernel_t;
+  (void)kernel_h;
+  const int32_t rc = na3d_check(reinterpret_cast<const void*>(16), reinterpret_cast<const void*>(16),
+                                reinterpret_cast<const void*>(16), reinterpret_cast<const void*>(16), 1, t, h, w,
+                                1, head_dim, kernel_t, kernel_h, kernel_w, 1.0f, nullptr);
+  if (rc != VX_OK) return rc;
+  const int32_t kw = kernel_w < w ? kernel_w : w;
+  if (kernel_name != nullptr && name_len > 0)
+    snprintf(kernel_name, (size_t)name_len, "%s", na3d_kernel_label(na3d_variant(kw, head_dim), head_dim));
+  return ok();
+}
 
 int32_t vx_flash_attn_check(const void* q, const void* k, const void* v, const void* out, const int32_t* kv_len,
                             const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride,
@@ -287,8 +435,10 @@ int32_t vx_flash_attn_fwd(const void* q, const void* k, const void* v, void* out
                            num_heads, head_dim, q_strides, k_strides, v_strides, out_strides, scale, &args);
   if (rc != VX_OK) return rc;
   if ((rc = injected()) != VX_OK) return rc;
-  const int err = vx::launch_flash_fwd(args, stream);
+  const char* launched = "";
+  const int err = vx::launch_flash_fwd(args, stream, &launched);
   if (err != 0) return fail(VX_ERR_LAUNCH, "flash attention launch failed (hipError_t %d)", err);
+  g_last_launch = launched;
   return ok();
 }
 
@@ -316,8 +466,10 @@ int32_t vx_flash_attn_bias_fwd(const void* q, const void* k, const void* v, void
                            bias_strides);
   if (rc != VX_OK) return rc;
   if ((rc = injected()) != VX_OK) return rc;
-  const int err = vx::launch_flash_fwd(args, stream);
+  const char* launched = "";
+  const int err = vx::launch_flash_fwd(args, stream, &launched);
   if (err != 0) return fail(VX_ERR_LAUNCH, "flash attention launch failed (hipError_t %d)", err);
+  g_last_launch = launched;
   return ok();
 }
 
@@ -335,8 +487,10 @@ int32_t vx_na3d_fwd(const void* q, const void* k, const void* v, void* out, int3
                           &args);
   if (rc != VX_OK) return rc;
   if ((rc = injected()) != VX_OK) return rc;
-  const int err = vx::launch_na3d_fwd(args, stream);
+  const char* launched = "";
+  const int err = vx::launch_na3d_fwd(args, stream, &launched);
   if (err != 0) return fail(VX_ERR_LAUNCH, "neighbourhood attention launch failed (hipError_t %d)", err);
+  g_last_launch = launched;
   return ok();
 }
 
@@ -375,8 +529,10 @@ int32_t vx_rmsnorm_scale_rope_fwd(const void* x, void* out, const float* weight,
                               seq, num_heads, head_dim, x_strides, out_strides, &args);
   if (rc != VX_OK) return rc;
   if ((rc = injected()) != VX_OK) return rc;
-  const int err = vx::launch_qk_prologue(args, stream);
+  const char* launched = "";
+  const int err = vx::launch_qk_prologue(args, stream, &launched);
   if (err != 0) return fail(VX_ERR_LAUNCH, "rmsnorm/rope launch failed (hipError_t %d)", err);
+  g_last_launch = launched;
   return ok();
 }
 

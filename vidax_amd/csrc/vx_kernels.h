@@ -23,6 +23,7 @@ struct FlashArgs {
   int32_t B, Sq, Sk, H, D;
   int64_t qs[3], ks[3], vs[3], os[3];
   float scale;  // softmax scale (> 0)
+  int32_t waves;  // workgroup size chosen by the launch plan: 4 (128 queries) or 8 (256)
 };
 
 // Neighbourhood attention launch arguments; tensors are contiguous
@@ -35,6 +36,15 @@ struct Na3dArgs {
   int32_t B, T, Hs, W, NH, D;
   int32_t kt, kh, kw;  // window sizes already clamped to the grid extents
   float scale;
+  int32_t variant;     // kernel chosen by the launch plan (Na3dVariant)
+};
+
+// Neighbourhood-attention kernels, by the clamped x window kw' and head dim.
+enum Na3dVariant : int32_t {
+  kNaPipe16 = 0,  // kw' <= 9: row streaming, 16-key x segments, 1 x 4 x 32 bricks
+  kNaTall = 1,    // 9 < kw' <= 13: the same body on 1 x 8 x 16 bricks
+  kNaPipe32 = 2,  // 13 < kw' <= 25: 32-key x segments
+  kNaWave = 3,    // 25 < kw' <= 57, head dim 128: per-wave bricks
 };
 
 struct PrologueArgs {
@@ -50,9 +60,11 @@ struct PrologueArgs {
   int64_t x_bstride, x_sstride, o_bstride, o_sstride, tab_stride;  // elements
 };
 
-// All return a hipError_t value (0 on success).
-int launch_flash_fwd(const FlashArgs& a, void* stream);
-int launch_na3d_fwd(const Na3dArgs& a, void* stream);
-int launch_qk_prologue(const PrologueArgs& a, void* stream);
+// All return a hipError_t value (0 on success) and store the name of the kernel they launched in *launched (a string with
+// static storage, built from the launched instantiation's template
+// arguments).
+int launch_flash_fwd(const FlashArgs& a, void* stream, const char** launched);
+int launch_na3d_fwd(const Na3dArgs& a, void* stream, const char** launched);
+int launch_qk_prologue(const PrologueArgs& a, void* stream, const char** launched);
 
 }  // namespace vx

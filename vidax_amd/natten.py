@@ -18,18 +18,16 @@ __all__ = ["neighborhood_attention_3d", "na3d_attention", "na3d_kernel_name"]
 
 
 def na3d_kernel_name(width: int, kernel_w: int, head_dim: int = 128) -> str:
-    """Name of the kernel the library launches for this x window (profiling aid):
-    the pipelined row-streaming kernel with 16-key x segments up to kw' = 9,
-    its tall-brick form (8 y x 4 x queries per wave) up to kw' = 13, 32-key
-    segments up to kw' = 25, the per-wave kernel above that (kw' = min(kw, W))."""
-    kw = min(int(kernel_w), int(width))
-    if kw <= 9:
-        return f"na3d_pipe_kernel<16, {head_dim}>"
-    if kw <= 13:
-        return f"na3d_tall_kernel<{head_dim}>"
-    if kw <= 25:
-        return f"na3d_pipe_kernel<32, {head_dim}>"
-    return "na3d_wave_kernel"
+    """Name of the kernel the library launches for this x window (the C ABI's
+    launch plan): row streaming with 16-key x segments up to kw' = 9, its
+    tall-brick form up to kw' = 13, 32-key segments up to kw' = 25, the
+    per-wave kernel above that (kw' = min(kw, W))."""
+    return _lib.na3d_plan(1, 1, int(width), int(head_dim), 1, 1, int(kernel_w))
+
+
+def _aligned16(t: torch.Tensor) -> torch.Tensor:
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
 def na3d_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -51,13 +49,15 @@ def na3d_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         raise ValueError("q, k and v must be on the same device")
     if len(kernel_size) != 3:
         raise ValueError("kernel_size must be (kt, kh, kw)")
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    # the kernel reads 16-byte chunks: contiguous tensors at 16-byte aligned
+    # addresses (a contiguous view at an odd offset is copied)
+    q, k, v = (_aligned16(t) for t in (q, k, v))
     B, T, H, W, NH, HD = q.shape
     if out is None:
         out = torch.empty_like(q)
     elif (out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous() or
-          out.device != q.device):
-        raise ValueError("out must be a contiguous bf16 tensor shaped like q, on q's device")
+          out.device != q.device or out.data_ptr() % 16 != 0):
+        raise ValueError("out must be a contiguous, 16-byte aligned bf16 tensor shaped like q, on q's device")
     stream = torch.cuda.current_stream(q.device).cuda_stream
     with torch.cuda.device(q.device):
         rc = _lib.lib().vx_na3d_fwd(
