@@ -42,6 +42,22 @@ WORKLOADS = {
                                                   seed=6),
                                      "3D neighbourhood attention 33x88x160, window (11,11,11), B=1 NH=4 D=64 "
                                      "(LTX-2.5 VAE stage 5 head layout)"),
+    "na3d_block_fused_q_21x45x80_H24": ("na3d_block", dict(B=1, T=21, Hs=45, W=80, NH=24, kernel=(3, 7, 7), seed=3,
+                                                          fused=True),
+                                        "NA block attention 21x45x80 (3,7,7) NH=24 D=128: q RMSNorm + "
+                                        "scale + abs RoPE inside the NA kernel"),
+    "na3d_block_two_pass_21x45x80_H24": ("na3d_block", dict(B=1, T=21, Hs=45, W=80, NH=24, kernel=(3, 7, 7),
+                                                            seed=3, fused=False),
+                                         "NA block attention 21x45x80 (3,7,7) NH=24 D=128: q prologue pass, "
+                                         "then the NA kernel"),
+    "na3d_block_fused_q_stage5_33x88x160_H4_D64": ("na3d_block", dict(B=1, T=33, Hs=88, W=160, NH=4, D=64,
+                                                                      kernel=(11, 11, 11), seed=6, fused=True),
+                                                   "NA block attention 33x88x160 (11,11,11) NH=4 D=64: q prep "
+                                                   "inside the NA kernel"),
+    "na3d_block_two_pass_stage5_33x88x160_H4_D64": ("na3d_block", dict(B=1, T=33, Hs=88, W=160, NH=4, D=64,
+                                                                       kernel=(11, 11, 11), seed=6, fused=False),
+                                                    "NA block attention 33x88x160 (11,11,11) NH=4 D=64: q "
+                                                    "prologue pass, then the NA kernel"),
     "qk_norm_rope_L32760_H40": ("prologue", dict(B=1, grid=(21, 30, 52), H=40, seed=5),
                                 "q and k RMSNorm(5120) + 3D RoPE, B=1 L=32760 (21x30x52) H=40 D=128"),
 }
@@ -127,6 +143,8 @@ def _cpu_baseline(kind, p, budget_s=12.0):
                   f"{Sk} keys, D=128) of this workload, {el:.1f} s")
         return {"value": round(flops / el / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads),
                 "kind": "port", "sample": sample}
+    if kind == "na3d_block":
+        kind = "na3d"
     if kind == "prologue":
         from oracle import prologue_oracle as P
         S, L = 2048, p["H"] * 128
@@ -246,6 +264,26 @@ def main(argv=None):
         def step():
             qk_norm_rope(qx, wq, freqs, p["H"])
             qk_norm_rope(kx, wk, freqs, p["H"])
+    elif kind == "na3d_block":
+        from vidax_amd import create_abs_rope3d_freqs, na3d_block_attention, na3d_qk_norm_rope
+        from vidax_amd import neighborhood_attention_3d
+        g = torch.Generator(device=dev)
+        g.manual_seed(p["seed"])
+        D = p.get("D", 128)
+        shape = (p["B"], p["T"], p["Hs"], p["W"], p["NH"], D)
+        q = (2.0 * torch.randn(shape, generator=g, device=dev)).to(torch.bfloat16)
+        k = torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)  # k as the block prepares it
+        v = torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)
+        wq = 1.0 + 0.1 * torch.randn(D, generator=g, device=dev)
+        freqs = create_abs_rope3d_freqs(p["T"], p["Hs"], p["W"], D, device=dev)
+        out = torch.empty_like(q)
+        flops, bytes_ = _na3d_work(p)
+        if p["fused"]:
+            def step():
+                na3d_block_attention(q, k, v, p["kernel"], wq, freqs, out=out)
+        else:
+            def step():
+                neighborhood_attention_3d(na3d_qk_norm_rope(q, wq, freqs, post_scale=D ** -0.5), k, v, p["kernel"])
     else:
         g = torch.Generator(device=dev)
         g.manual_seed(p["seed"])

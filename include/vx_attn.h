@@ -155,6 +155,41 @@ int32_t vx_na3d_check(const void* q, const void* k, const void* v, const void* o
                       float scale);
 
 /*
+ * vx_na3d_fwd with the neighbourhood-attention block's q preparation done by
+ * the kernel as it loads each query row (q is read once, as projected):
+ *   if q_norm_weight != NULL: per-head RMSNorm over head_dim,
+ *                     y = bf16(bf16(q * rsqrt(mean(q^2) + eps)) * bf16(w[d]))
+ *                     with fp32 statistics (q_norm_weight fp32[head_dim])
+ *   if q_post_scale != 1:  y = bf16(y * bf16(q_post_scale))
+ *   if rope_cos != NULL:   adjacent pairs (y[2j], y[2j+1]) rotated by the
+ *                     token's (rope_cos[s*rope_stride + j], rope_sin[...]) in
+ *                     fp32, rounded to bf16; s = (t*h + y)*w + x
+ * then out = neighbourhood attention of (y, k, v) with logit scale 1, as
+ * vx_na3d_fwd. The rounding points are vx_rmsnorm_scale_rope_fwd's (with
+ * per_head_norm = 1); k and v are passed as the block prepares them (k
+ * normed and rotated by vx_rmsnorm_scale_rope_fwd). Tables as for that
+ * call: fp32, 16-byte aligned, rope_stride a multiple of 4 and >= head_dim/2.
+ * Limits and layouts otherwise those of vx_na3d_fwd.
+ *
+ * Replaces the q half of src/vidax/models/ltx2_5/diffusion_vae.py:263-277
+ * (q_norm, q * head_dim**-0.5, _apply_abs_rope(q, ...), then
+ * neighborhood_attention_3d), with the tables of _rope_inv_freqs /
+ * _default_rope_dim_split (:96-109).
+ */
+int32_t vx_na3d_qprep_fwd(const void* q, const void* k, const void* v, void* out, int32_t batch, int32_t t,
+                          int32_t h, int32_t w, int32_t num_heads, int32_t head_dim, int32_t kernel_t,
+                          int32_t kernel_h, int32_t kernel_w, const float* q_norm_weight, float eps,
+                          float q_post_scale, const float* rope_cos, const float* rope_sin, int64_t rope_stride,
+                          void* stream);
+
+/* Host-only argument check for vx_na3d_qprep_fwd (no GPU needed). */
+int32_t vx_na3d_qprep_check(const void* q, const void* k, const void* v, const void* out, int32_t batch, int32_t t,
+                            int32_t h, int32_t w, int32_t num_heads, int32_t head_dim, int32_t kernel_t,
+                            int32_t kernel_h, int32_t kernel_w, const float* q_norm_weight, float eps,
+                            float q_post_scale, const float* rope_cos, const float* rope_sin,
+                            int64_t rope_stride);
+
+/*
  * Fused attention prologue: RMSNorm and/or 3D rotary embedding of q or k in
  * one pass (read x once, write out once), bf16 in and out. For each token row
  * (num_heads * head_dim values, contiguous):

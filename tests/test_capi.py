@@ -397,3 +397,30 @@ def test_na3d_inputs_are_realigned():
     assert fixed.data_ptr() % 16 == 0 and torch.equal(fixed, view)
     good = buf[8:8 + 64].view(1, 1, 1, 2, 4, 8)
     assert _aligned16(good) is good
+
+
+def _qprep_check(**kw):
+    args = dict(q=A, w=A, eps=1e-6, post=0.125, cos=A, sin=A, stride=64, D=128, kw=7)
+    args.update(kw)
+    return _lib.lib().vx_na3d_qprep_check(args["q"], A, A, A, 1, 3, 8, 80, 2, args["D"], 3, 7, args["kw"],
+                                          args["w"], ctypes.c_float(args["eps"]), ctypes.c_float(args["post"]),
+                                          args["cos"], args["sin"], args["stride"])
+
+
+def test_na3d_qprep_check():
+    assert _qprep_check() == _lib.VX_OK
+    assert _qprep_check(w=None, cos=None, sin=None, post=1.0) == _lib.VX_OK   # plain NA
+    assert _qprep_check(D=64, stride=32) == _lib.VX_OK
+    for kw, code, frag in [
+        (dict(w=A + 4), _lib.VX_ERR_INVALID_ARGUMENT, "q_norm_weight"),
+        (dict(eps=-1.0), _lib.VX_ERR_INVALID_ARGUMENT, "eps"),
+        (dict(post=float("nan")), _lib.VX_ERR_INVALID_ARGUMENT, "q_post_scale"),
+        (dict(sin=None), _lib.VX_ERR_INVALID_ARGUMENT, "both"),
+        (dict(cos=A + 8), _lib.VX_ERR_INVALID_ARGUMENT, "aligned"),
+        (dict(stride=62), _lib.VX_ERR_INVALID_ARGUMENT, "rope_stride"),
+        (dict(stride=60), _lib.VX_ERR_INVALID_ARGUMENT, "rope_stride"),
+        (dict(q=None), _lib.VX_ERR_INVALID_ARGUMENT, "non-NULL"),
+        (dict(kw=60), _lib.VX_ERR_UNSUPPORTED, "57"),
+    ]:
+        assert _qprep_check(**kw) == code, kw
+        assert frag in _lib.last_error(), (kw, _lib.last_error())

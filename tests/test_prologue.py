@@ -371,3 +371,57 @@ def test_abs_rope_tables_and_apply_match_oracle(gpu):
     out = apply_abs_rope3d(_dev(x, gpu), (cos, sin))
     torch.cuda.synchronize()
     _check(out.float().cpu().numpy(), P.apply_abs_rope3d(x), "apply_abs_rope3d")
+
+
+# ------------------- NA block with q prepared inside the attention kernel
+NA_BLOCK_CASES = [
+    # (B, (T, H, W), NH, HD, kernel, norm, rope)  -> launched kernel family
+    (1, (3, 8, 20), 4, 64, (3, 7, 7), True, True),        # pipe, 16-key segments, D=64
+    (1, (3, 9, 37), 2, 128, (3, 7, 7), True, True),       # pipe, D=128, ragged x
+    (1, (5, 13, 21), 2, 64, (5, 11, 11), True, True),     # tall bricks (stage-5 family), D=64
+    (1, (2, 7, 30), 8, 128, (1, 3, 17), True, True),      # 32-key segments, head remap (NH % 8 == 0)
+    (1, (2, 4, 40), 1, 128, (1, 3, 31), True, True),      # per-wave kernel (kw' > 25)
+    (2, (2, 5, 9), 3, 64, (3, 3, 5), False, True),        # rope only
+    (1, (2, 6, 10), 2, 128, (3, 5, 5), True, False),      # norm and scale only
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,grid,NH,HD,ks,norm,rope", NA_BLOCK_CASES)
+def test_na3d_block_attention_fused_q(gpu, B, grid, NH, HD, ks, norm, rope):
+    """The block's q preparation (per-head RMSNorm, * head_dim**-0.5 in bf16,
+    absolute RoPE; diffusion_vae.py:263-277) done inside the NA kernel as it
+    loads q: against the oracle (prologue oracle, then the NA oracle) at the
+    attention bar, and bit for bit against the separate path (the one-pass
+    prologue kernel, then the NA kernel), whose rounding points and
+    per-head summation order the fused kernel reproduces."""
+    from vidax_amd import (create_abs_rope3d_freqs, na3d_block_attention, na3d_qk_norm_rope,
+                           neighborhood_attention_3d)
+    from vidax_amd import _lib
+    print(f"[case] na3d fused q B={B} grid={grid} NH={NH} HD={HD} kernel={ks} norm={norm} rope={rope}", flush=True)
+    rng = np.random.default_rng(sum(grid) * NH + HD + ks[2])
+    shape = (B, *grid, NH, HD)
+    q = _bf16_normal(rng, shape, 2.0)
+    k_raw = _bf16_normal(rng, shape, 2.0)
+    v = _bf16_normal(rng, shape)
+    wq = (1.0 + 0.3 * rng.standard_normal(HD)).astype(np.float32) if norm else None
+    wk = (1.0 + 0.3 * rng.standard_normal(HD)).astype(np.float32) if norm else None
+    post = HD ** -0.5
+    freqs = create_abs_rope3d_freqs(*grid, HD, device=gpu) if rope else None
+    tq, tv = _dev(q, gpu), _dev(v, gpu)
+    tw = torch.from_numpy(wq).to(gpu) if norm else None
+    tk = na3d_qk_norm_rope(_dev(k_raw, gpu), torch.from_numpy(wk).to(gpu) if norm else None, freqs)
+    fused = na3d_block_attention(tq, tk, tv, ks, tw, freqs)
+    launched = _lib.last_launch()
+    separate = neighborhood_attention_3d(na3d_qk_norm_rope(tq, tw, freqs, post_scale=post), tk, tv, ks)
+    torch.cuda.synchronize()
+    print(f"  launched {launched}", flush=True)
+    assert launched == _lib.last_launch()
+    assert torch.equal(fused, separate), "fused q preparation differs from the two-pass path"
+    q_ref = P.na3d_qk_norm_rope(q, wq, post_scale=post, rope=rope)
+    k_ref = tk.float().cpu().numpy()
+    ref = A.na3d(q_ref, k_ref, v, ks)
+    o = fused.float().cpu().numpy()
+    d = np.abs(o - ref)
+    print(f"  vs oracle: max_abs={d.max():.3e} mean_abs={d.mean():.3e}", flush=True)
+    assert d.max() <= 2e-2 and d.mean() <= 2e-3

@@ -13,7 +13,7 @@ all backed by libvx_attn.so (C ABI: include/vx_attn.h).
 """
 from .attention import (dot_product_attention, flash_attention, local_attention,
                         masked_self_attention)
-from .natten import neighborhood_attention_3d
+from .natten import na3d_block_attention, neighborhood_attention_3d
 from .prologue import (apply_abs_rope3d, apply_rope3d, create_abs_rope3d_freqs, create_rope3d_freqs,
                        default_rope_dim_split, na3d_qk_norm_rope, qk_norm_rope, rms_norm)
 
@@ -23,6 +23,7 @@ __all__ = [
     "local_attention",
     "masked_self_attention",
     "neighborhood_attention_3d",
+    "na3d_block_attention",
     "rms_norm",
     "create_rope3d_freqs",
     "apply_rope3d",

@@ -36,6 +36,8 @@ EXPORTED_SYMBOLS = (
     "vx_flash_attn_plan",
     "vx_na3d_plan",
     "vx_last_launch",
+    "vx_na3d_qprep_fwd",
+    "vx_na3d_qprep_check",
 )
 
 _lock = threading.Lock()
@@ -52,6 +54,7 @@ _FLASH_ARGS = [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32,
 _NA3D_ARGS = [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32]
 _FLASH_BIAS_ARGS = [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64p, _i32, _i32, _i32, _i32, _i32,
                     _i64p, _i64p, _i64p, _i64p, _f32]
+_NA3D_QPREP_ARGS = [_p, _p, _p, _p] + [_i32] * 9 + [_p, _f32, _f32, _p, _p, _i64]
 _PROLOGUE_ARGS = [_p, _p, _p, _f32, _i32, _p, _p, _i64, _i32, _i32, _i32, _i32, _i64p, _i64p]
 _SCALED_PROLOGUE_ARGS = _PROLOGUE_ARGS[:5] + [_f32] + _PROLOGUE_ARGS[5:]
 
@@ -108,6 +111,10 @@ def lib() -> ctypes.CDLL:
             h.vx_flash_attn_plan.argtypes = [_i32] * 6 + [ctypes.c_char_p, _i32]
             h.vx_na3d_plan.restype = _i32
             h.vx_na3d_plan.argtypes = [_i32] * 7 + [ctypes.c_char_p, _i32]
+            h.vx_na3d_qprep_fwd.restype = _i32
+            h.vx_na3d_qprep_fwd.argtypes = _NA3D_QPREP_ARGS + [_p]
+            h.vx_na3d_qprep_check.restype = _i32
+            h.vx_na3d_qprep_check.argtypes = _NA3D_QPREP_ARGS
             h.vx_last_launch.restype = ctypes.c_char_p
             h.vx_last_launch.argtypes = []
             _lib = h

@@ -24,6 +24,7 @@
 // kt' x kh' x kw' window.
 #include "vx_gfx950.hpp"
 #include "vx_kernels.h"
+#include "vx_qk_prep.hpp"
 
 namespace vx {
 namespace {
@@ -44,6 +45,66 @@ __device__ __forceinline__ int row_swizzle(int r) { return ((r & 3) << 1) | ((r 
 
 __device__ __forceinline__ int window_start(int i, int len, int k) {
   return min(max(i - k / 2, 0), len - k);
+}
+
+// The block's q preparation on the resident Q fragments of one lane (query
+// `tok`, d = 16 * ds + 8 * hf + 0..7 in qr[ds]; lane l ^ 32 holds the other
+// half of the row), with the rounding points of the one-pass prologue kernel.
+// The per-head sum of squares adds the 8-element chunk sums in the order of
+// that kernel's xor-butterfly over the head's D/8 chunks (chunk c = 2*ds+hf
+// pairs with c^8, c^4, c^2 inside the lane and with c^1 in the other half).
+template <int NDS>
+__device__ __forceinline__ void prep_q(bf16x8 (&qr)[NDS], int hf, int64_t tok, const Na3dArgs& a) {
+  constexpr int D = NDS * 16;
+  // all loads first (weights, then the token's rotation tables), so their
+  // latencies overlap
+  f32x4 w[NDS][2], cs[NDS], sn[NDS];
+  const bool norm = (a.q_prep & kQPrepNorm) != 0, rope = (a.q_prep & kQPrepRope) != 0;
+  if (norm) {
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
+      const float* wp = a.q_weight + ds * 16 + hf * 8;
+      w[ds][0] = *(const f32x4*)wp;
+      w[ds][1] = *(const f32x4*)(wp + 4);
+    }
+  }
+  if (rope) {
+    const float* cr = a.q_cos + tok * a.q_tab_stride + hf * 4;
+    const float* sr = a.q_sin + tok * a.q_tab_stride + hf * 4;
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
+      cs[ds] = *(const f32x4*)(cr + ds * 8);
+      sn[ds] = *(const f32x4*)(sr + ds * 8);
+    }
+  }
+  if (norm) {
+    float ss[NDS];
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) ss[ds] = sum_sq8(qr[ds]);
+    // level m adds ds and ds + m (m = NDS/2, ..., 1); ss[0] ends with the sum
+#pragma unroll
+    for (int m = NDS / 2; m >= 1; m >>= 1)
+#pragma unroll
+      for (int ds = 0; ds < m; ++ds) ss[ds] = ss[ds] + ss[ds + m];
+    const float rinv = rms_inv(halves_sum(ss[0]), D, a.q_eps);
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qr[ds][e] = rms_elem((float)qr[ds][e], rinv, w[ds][e >> 2][e & 3]);
+  }
+  if (a.q_prep & kQPrepScale) {
+    const float ps = (float)(bf16)a.q_post_scale;
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qr[ds][e] = scale_elem((float)qr[ds][e], ps);
+  }
+  if (rope) {
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds)
+#pragma unroll
+      for (int p = 0; p < 4; ++p) rope_pair(qr[ds], p, cs[ds][p], sn[ds][p]);
+  }
 }
 
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
@@ -101,6 +162,7 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
 #pragma unroll
     for (int ds = 0; ds < 8; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
   }
+  if (a.q_prep != 0) prep_q(qr, hf, token(t, yqc, xqc), a);
 
   // Token index of key j of a 16-key half chunk starting at box key kb2.
   auto half_row = [&](int kb2, int& trow, int& j0) {
@@ -492,6 +554,8 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   issue(kg, C::kK + C::kSlot, kcur);
   for (int off = threadIdx.x * 16; off < C::kSlot; off += C::kThreads * 16)
     *(VX_LDS u32x4*)(lds + C::kV + C::kSlot + off) = u32x4{0, 0, 0, 0};
+  // q preparation while the first key rows land (its loads overlap theirs)
+  if (a.q_prep != 0) prep_q(qr, hf, token(t, yqc, xqc), a);
   wait_vmem<0>();
   __syncthreads();
   f32x16 S = f32x16{};

@@ -20,6 +20,7 @@
 // of the row, so every load and store is one coalesced 1 KiB wave access.
 #include "vx_gfx950.hpp"
 #include "vx_kernels.h"
+#include "vx_qk_prep.hpp"
 
 #include <string>
 
@@ -40,8 +41,6 @@ __device__ __forceinline__ float group_sum(float v, int n) {
   for (int off = n >> 1; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
-
-__device__ __forceinline__ float rsqrt_ieee(float x) { return 1.0f / __builtin_sqrtf(x); }
 
 __device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
 
@@ -68,8 +67,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const 
     ss[i] = 0.f;
     if (live(c)) {
       v[i] = __builtin_nontemporal_load((const bf16x8*)(xr + c * 8));  // read once: streaming
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss[i] = __builtin_fmaf((float)v[i][e], (float)v[i][e], ss[i]);
+      ss[i] = sum_sq8(v[i]);
     }
   }
 
@@ -79,23 +77,19 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const 
       float t = 0.f;
 #pragma unroll
       for (int i = 0; i < NCHUNK; ++i) t += ss[i];
-      rinv_row = rsqrt_ieee(wave_sum(t) / (float)row_len + a.eps);
+      rinv_row = rms_inv(wave_sum(t), row_len, a.eps);
     }
 #pragma unroll
     for (int i = 0; i < NCHUNK; ++i) {
       const int c = lane + 64 * i;
       // per head: the head_dim / 8 lanes of an aligned group share a head
       float rinv = rinv_row;
-      if (a.per_head) rinv = rsqrt_ieee(group_sum(ss[i], a.D / 8) / (float)a.D + a.eps);
+      if (a.per_head) rinv = rms_inv(group_sum(ss[i], a.D / 8), a.D, a.eps);
       if (live(c)) {
         const f32x4 w0 = *(const f32x4*)(a.weight + c * 8);
         const f32x4 w1 = *(const f32x4*)(a.weight + c * 8 + 4);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float n = (float)to_bf16((float)v[i][e] * rinv);
-          const float w = (float)to_bf16(e < 4 ? w0[e] : w1[e - 4]);
-          v[i][e] = to_bf16(n * w);
-        }
+        for (int e = 0; e < 8; ++e) v[i][e] = rms_elem((float)v[i][e], rinv, e < 4 ? w0[e] : w1[e - 4]);
       }
     }
   }
@@ -106,7 +100,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const 
     for (int i = 0; i < NCHUNK; ++i) {
       if (live(lane + 64 * i)) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[i][e] = to_bf16((float)v[i][e] * ps);
+        for (int e = 0; e < 8; ++e) v[i][e] = scale_elem((float)v[i][e], ps);
       }
     }
   }
@@ -122,11 +116,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const 
         const f32x4 cs = *(const f32x4*)(cr + j0);
         const f32x4 sn = *(const f32x4*)(sr + j0);
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const float x1 = (float)v[i][2 * p], x2 = (float)v[i][2 * p + 1];
-          v[i][2 * p] = to_bf16(x1 * cs[p] - x2 * sn[p]);
-          v[i][2 * p + 1] = to_bf16(x2 * cs[p] + x1 * sn[p]);
-        }
+        for (int p = 0; p < 4; ++p) rope_pair(v[i], p, cs[p], sn[p]);
       }
     }
   }

@@ -301,8 +301,49 @@ int32_t na3d_check(const void* q, const void* k, const void* v, const void* out,
     args->kw = kw < W ? kw : W;
     args->scale = scale;
     args->variant = na3d_variant(args->kw, D);
+    args->q_prep = 0;
+    args->q_weight = nullptr;
+    args->q_cos = args->q_sin = nullptr;
+    args->q_eps = 0.f;
+    args->q_post_scale = 1.f;
+    args->q_tab_stride = 0;
   }
   return ok();
+}
+
+// The q-preparation arguments of vx_na3d_qprep_fwd, checked into a.
+int32_t na3d_qprep_check(const float* weight, float eps, float post_scale, const float* rope_cos,
+                         const float* rope_sin, int64_t rope_stride, int32_t D, vx::Na3dArgs* args) {
+  int32_t prep = 0;
+  if (weight != nullptr) {
+    if (!aligned16(weight)) return fail(VX_ERR_INVALID_ARGUMENT, "q_norm_weight must be 16-byte aligned");
+    if (!(eps >= 0.f) || !std::isfinite(eps))
+      return fail(VX_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0 (got %g)", (double)eps);
+    prep |= vx::kQPrepNorm;
+  }
+  if (!std::isfinite(post_scale))
+    return fail(VX_ERR_INVALID_ARGUMENT, "q_post_scale must be finite (got %g)", (double)post_scale);
+  if (post_scale != 1.0f) prep |= vx::kQPrepScale;
+  if ((rope_cos == nullptr) != (rope_sin == nullptr))
+    return fail(VX_ERR_INVALID_ARGUMENT, "rope_cos and rope_sin must both be given or both be NULL");
+  if (rope_cos != nullptr) {
+    if (!aligned16(rope_cos) || !aligned16(rope_sin))
+      return fail(VX_ERR_INVALID_ARGUMENT, "rope_cos and rope_sin must be 16-byte aligned");
+    if (rope_stride < D / 2 || rope_stride % 4 != 0)
+      return fail(VX_ERR_INVALID_ARGUMENT, "rope_stride (%lld) must be a multiple of 4 and >= head_dim / 2 = %d",
+                  (long long)rope_stride, D / 2);
+    prep |= vx::kQPrepRope;
+  }
+  if (args != nullptr) {
+    args->q_prep = prep;
+    args->q_weight = weight;
+    args->q_eps = eps;
+    args->q_post_scale = post_scale;
+    args->q_cos = rope_cos;
+    args->q_sin = rope_sin;
+    args->q_tab_stride = rope_stride;
+  }
+  return VX_OK;
 }
 
 int32_t prologue_check(const void* x, const void* out, const float* weight, float eps, int32_t per_head,
@@ -486,6 +527,39 @@ int32_t vx_na3d_fwd(const void* q, const void* k, const void* v, void* out, int3
   int32_t rc = na3d_check(q, k, v, out, batch, t, h, w, num_heads, head_dim, kernel_t, kernel_h, kernel_w, scale,
                           &args);
   if (rc != VX_OK) return rc;
+  if ((rc = injected()) != VX_OK) return rc;
+  const char* launched = "";
+  const int err = vx::launch_na3d_fwd(args, stream, &launched);
+  if (err != 0) return fail(VX_ERR_LAUNCH, "neighbourhood attention launch failed (hipError_t %d)", err);
+  g_last_launch = launched;
+  return ok();
+}
+
+int32_t vx_na3d_qprep_check(const void* q, const void* k, const void* v, const void* out, int32_t batch, int32_t t,
+                            int32_t h, int32_t w, int32_t num_heads, int32_t head_dim, int32_t kernel_t,
+                            int32_t kernel_h, int32_t kernel_w, const float* q_norm_weight, float eps,
+                            float q_post_scale, const float* rope_cos, const float* rope_sin, int64_t rope_stride) {
+  int32_t rc = na3d_check(q, k, v, out, batch, t, h, w, num_heads, head_dim, kernel_t, kernel_h, kernel_w, 1.0f,
+                          nullptr);
+  if (rc != VX_OK) return rc;
+  if ((rc = na3d_qprep_check(q_norm_weight, eps, q_post_scale, rope_cos, rope_sin, rope_stride, head_dim,
+                             nullptr)) != VX_OK)
+    return rc;
+  return ok();
+}
+
+int32_t vx_na3d_qprep_fwd(const void* q, const void* k, const void* v, void* out, int32_t batch, int32_t t,
+                          int32_t h, int32_t w, int32_t num_heads, int32_t head_dim, int32_t kernel_t,
+                          int32_t kernel_h, int32_t kernel_w, const float* q_norm_weight, float eps,
+                          float q_post_scale, const float* rope_cos, const float* rope_sin, int64_t rope_stride,
+                          void* stream) {
+  vx::Na3dArgs args;
+  int32_t rc = na3d_check(q, k, v, out, batch, t, h, w, num_heads, head_dim, kernel_t, kernel_h, kernel_w, 1.0f,
+                          &args);
+  if (rc != VX_OK) return rc;
+  if ((rc = na3d_qprep_check(q_norm_weight, eps, q_post_scale, rope_cos, rope_sin, rope_stride, head_dim,
+                             &args)) != VX_OK)
+    return rc;
   if ((rc = injected()) != VX_OK) return rc;
   const char* launched = "";
   const int err = vx::launch_na3d_fwd(args, stream, &launched);

@@ -37,7 +37,20 @@ struct Na3dArgs {
   int32_t kt, kh, kw;  // window sizes already clamped to the grid extents
   float scale;
   int32_t variant;     // kernel chosen by the launch plan (Na3dVariant)
+  // q preparation applied by the kernel as it loads q (0 = q is used as
+  // given): bit 1 per-head RMSNorm with q_weight[D] and q_eps, bit 2 times
+  // bf16(q_post_scale), bit 4 rotation of adjacent pairs by the token's
+  // (q_cos, q_sin) row (token t*Hs*W + y*W + x, D/2 fp32 values at
+  // q_tab_stride)
+  int32_t q_prep;
+  const float* q_weight;
+  float q_eps;
+  float q_post_scale;
+  const float* q_cos;
+  const float* q_sin;
+  int64_t q_tab_stride;
 };
+constexpr int32_t kQPrepNorm = 1, kQPrepScale = 2, kQPrepRope = 4;
 
 // Neighbourhood-attention kernels, by the clamped x window kw' and head dim.
 enum Na3dVariant : int32_t {

@@ -14,7 +14,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["neighborhood_attention_3d", "na3d_attention", "na3d_kernel_name"]
+__all__ = ["neighborhood_attention_3d", "na3d_attention", "na3d_kernel_name", "na3d_block_attention"]
 
 
 def na3d_kernel_name(width: int, kernel_w: int, head_dim: int = 128) -> str:
@@ -72,3 +72,56 @@ def neighborhood_attention_3d(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                               kernel_size: Tuple[int, int, int]) -> torch.Tensor:
     """NATTEN-semantics 3D neighbourhood attention; q is pre-scaled by the caller."""
     return na3d_attention(q, k, v, kernel_size, scale=1.0)
+
+
+def na3d_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                         kernel_size: Tuple[int, int, int], q_norm_weight: Optional[torch.Tensor], freqs,
+                         eps: float = 1e-6, q_post_scale: Optional[float] = None,
+                         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention of the LTX-2.5 neighbourhood-attention block with q prepared
+    inside the kernel (`src/vidax/models/ltx2_5/diffusion_vae.py:263-277`):
+    q as projected (B, T, H, W, NH, HD) goes through per-head RMSNorm with
+    `q_norm_weight` (HD,) (skipped when None), times bf16(q_post_scale)
+    (default HD ** -0.5, the block's `q * head_dim ** -0.5`), and the absolute
+    RoPE with `freqs` from `create_abs_rope3d_freqs` (skipped when None), as
+    the kernel loads each query row; k (normed and rotated, e.g. by
+    `na3d_qk_norm_rope`) and v are used as given. Equals
+    `neighborhood_attention_3d(na3d_qk_norm_rope(q, ...), k, v, kernel_size)`
+    without the separate pass over q."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor) or t.dim() != 6 or t.dtype != torch.bfloat16 or not t.is_cuda:
+            raise ValueError(f"{name} must be a (B, T, H, W, NH, HD) bf16 GPU tensor")
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k and v must have the same shape")
+    if len(kernel_size) != 3:
+        raise ValueError("kernel_size must be (kt, kh, kw)")
+    q, k, v = (_aligned16(t) for t in (q, k, v))
+    B, T, H, W, NH, HD = q.shape
+    if q_post_scale is None:
+        q_post_scale = HD ** -0.5
+    weight = None
+    if q_norm_weight is not None:
+        weight = torch.as_tensor(q_norm_weight, device=q.device).to(torch.float32).reshape(-1).contiguous()
+        if weight.numel() != HD:
+            raise ValueError(f"q_norm_weight has {weight.numel()} entries, head_dim is {HD}")
+    cos_t = sin_t = None
+    stride = 0
+    if freqs is not None:
+        from .prologue import _tables
+        cos_t, sin_t, stride = _tables(freqs, T * H * W, HD // 2, q.device)
+    if out is None:
+        out = torch.empty_like(q)
+    elif (out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous() or
+          out.device != q.device or out.data_ptr() % 16 != 0):
+        raise ValueError("out must be a contiguous, 16-byte aligned bf16 tensor shaped like q, on q's device")
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    with torch.cuda.device(q.device):
+        rc = _lib.lib().vx_na3d_qprep_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            B, T, H, W, NH, HD, int(kernel_size[0]), int(kernel_size[1]), int(kernel_size[2]),
+            weight.data_ptr() if weight is not None else None, ctypes.c_float(eps),
+            ctypes.c_float(q_post_scale),
+            cos_t.data_ptr() if cos_t is not None else None,
+            sin_t.data_ptr() if sin_t is not None else None, stride, ctypes.c_void_p(stream))
+    _lib.raise_for(rc)
+    return out
