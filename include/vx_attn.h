@@ -78,6 +78,43 @@ int32_t vx_flash_attn_fwd(const void* q, const void* k, const void* v, void* out
                           void* stream);
 
 /*
+ * vx_flash_attn_fwd with a caller-provided device workspace (no other
+ * argument differs). When a grid's last round of workgroups would leave
+ * most of the device idle (e.g. 732 workgroups of 128 queries over 512
+ * resident ones), the query tiles of that round are each computed as two
+ * workgroups over the two halves of the keys, whose fp32 partial results go
+ * to the workspace and are merged by a second kernel on the same stream.
+ * That needs vx_flash_attn_workspace_size() bytes (0: no split for this
+ * shape on this device); with a smaller workspace (or NULL) the call runs
+ * without the split, as vx_flash_attn_fwd. The workspace must be 16-byte
+ * aligned and stay untouched until the work on `stream` has finished; calls
+ * that overlap on different streams need different workspaces.
+ * Replaces the same reference call sites as vx_flash_attn_fwd.
+ */
+int32_t vx_flash_attn_ws_fwd(const void* q, const void* k, const void* v, void* out, const int32_t* kv_len,
+                             const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride,
+                             int32_t batch, int32_t seq_q, int32_t seq_k, int32_t num_heads, int32_t head_dim,
+                             const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                             const int64_t* out_strides, float scale, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
+/*
+ * Workspace bytes vx_flash_attn_ws_fwd uses for this shape on the current
+ * device (0 when it does not split, or on failure). Head dim 64 or 128.
+ */
+int64_t vx_flash_attn_workspace_size(int32_t batch, int32_t seq_q, int32_t seq_k, int32_t num_heads,
+                                     int32_t head_dim);
+
+/*
+ * The key-split plan of vx_flash_attn_ws_fwd for a device with num_cus
+ * compute units (host only, no GPU): the number of query-tile items split
+ * in two, the first key of the second half, and the workspace bytes.
+ */
+int32_t vx_flash_attn_split_plan(int32_t batch, int32_t seq_q, int32_t seq_k, int32_t num_heads, int32_t head_dim,
+                                 int32_t num_cus, int32_t* split_items, int32_t* split_key,
+                                 int64_t* workspace_bytes);
+
+/*
  * vx_flash_attn_fwd plus an additive fp32 bias that depends on the head and
  * the query as well as the key (T5's relative-position bias, causal or other
  * boolean masks turned into 0 / -inf):

@@ -424,3 +424,36 @@ def test_na3d_qprep_check():
     ]:
         assert _qprep_check(**kw) == code, kw
         assert frag in _lib.last_error(), (kw, _lib.last_error())
+
+
+def _split(shape, cus=256):
+    a, b, c = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    rc = _lib.lib().vx_flash_attn_split_plan(*shape, cus, ctypes.byref(a), ctypes.byref(b), ctypes.byref(c))
+    assert rc == _lib.VX_OK
+    return a.value, b.value, c.value
+
+
+def test_flash_split_plan():
+    """Key split of a grid's last round: only when that round holds at most
+    half the resident workgroups and the keys span >= 16 tiles; the workspace
+    holds two fp32 partials (O, reference point, row sum per lane) per item."""
+    # c1: 61 x 12 = 732 items of 128 queries over 2 x 256 slots: 220 split at tile 61
+    assert _split((1, 7800, 7800, 12, 128)) == (220, 61 * 64, 2 * 220 * 4 * 64 * (4 * 16 + 2) * 4)
+    assert _split((1, 32760, 32760, 40, 128)) == (0, 0, 0)     # 5120 items: whole rounds
+    assert _split((2, 32760, 512, 40, 128)) == (0, 0, 0)       # short keys
+    assert _split((1, 119056, 119056, 24, 128)) == (0, 0, 0)   # last round 176 > 128 of 256
+    assert _split((1, 2048, 1500, 3, 128)) == (48, 768, 2 * 48 * 4 * 64 * 66 * 4)
+    assert _split((1, 8192, 2048, 25, 128))[0] == 32            # 8-wave: 800 items, 256 slots
+    assert _split((1, 8192, 2048, 25, 64))[2] == 2 * 32 * 8 * 64 * (2 * 16 + 2) * 4
+    assert _split((1, 7800, 7800, 12, 128), cus=0) == (0, 0, 0)
+    assert _split((1, 7800, 900, 12, 128)) == (0, 0, 0)        # 15 key tiles
+
+
+def test_ws_fwd_rejects_before_launch():
+    L = _lib.lib()
+    args = [A, A, A, A, None, None, None, 0, 1, 100, 200, 4, 128, None, None, None, None, ctypes.c_float(0.1)]
+    assert L.vx_flash_attn_ws_fwd(*args, A + 8, 1024, None) == _lib.VX_ERR_INVALID_ARGUMENT
+    assert "workspace" in _lib.last_error()
+    assert L.vx_flash_attn_ws_fwd(*args, A, -1, None) == _lib.VX_ERR_INVALID_ARGUMENT
+    args[12] = 96
+    assert L.vx_flash_attn_ws_fwd(*args, A, 1024, None) == _lib.VX_ERR_UNSUPPORTED

@@ -177,8 +177,11 @@ def test_flash_config1_full(gpu):
     """Wan2.1-1.3B self-attention, B=1 H=12 L=7800 D=128, seed 0, whole output."""
     from vidax_amd import flash_attention
     _say("flash c1 full B=1 H=12 L=7800")
+    from vidax_amd import _lib
     q, k, v, _ = O.make_flash_inputs(1, 7800, 7800, 12, 128, 0)
     out = flash_attention(_t(q, gpu), _t(k, gpu), _t(v, gpu))
+    # 732 workgroups for 512 resident ones: the last 220 run split over the key halves
+    assert _lib.last_launch() == "flash_fwd_split_kernel<0, 128, 4>", _lib.last_launch()
     ref = O.attention(q, k, v, acc=np.float32)
     _check(out, ref, "c1")
 
@@ -551,5 +554,87 @@ def test_flash_forced_block_sizes(gpu, block_q, shape):
     assert res.returncode == 0, res.stdout[-2000:]
     r = json.loads(res.stdout.strip().splitlines()[-1])
     print(f"  {r}", flush=True)
-    assert r["name"] == f"flash_fwd_kernel<0, {shape[4]}, {block_q // 32}>"
+    # (small grids also split their keys: the split form of the same kernel)
+    assert r["name"] in (f"flash_fwd_kernel<0, {shape[4]}, {block_q // 32}>",
+                         f"flash_fwd_split_kernel<0, {shape[4]}, {block_q // 32}>"), r["name"]
     assert r["max"] <= MAX_ABS and r["mean"] <= MEAN_ABS
+
+
+# ------------------------------------------------ key split of the last round
+def _plain_flash(q, k, v, kw, scale=None):
+    """The same call through vx_flash_attn_fwd, which never splits."""
+    import ctypes
+    from vidax_amd import _lib
+    from vidax_amd.attention import _mask_rows
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    out = torch.empty_like(q)
+    kvl = kw.get("kv_len")
+    kvd = _mask_rows(kw["key_valid"].to(torch.bool), Sk, torch.uint8, 0) if "key_valid" in kw else None
+    kbs = _mask_rows(kw["key_bias"].float(), Sk, torch.float32, float("-inf")) if "key_bias" in kw else None
+    stride = (kvd if kvd is not None else kbs).shape[1] if (kvd is not None or kbs is not None) else 0
+    rc = _lib.lib().vx_flash_attn_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+        kvl.data_ptr() if kvl is not None else None, kvd.data_ptr() if kvd is not None else None,
+        kbs.data_ptr() if kbs is not None else None, stride, B, Sq, Sk, H, D, None, None, None, None,
+        ctypes.c_float(scale if scale is not None else D ** -0.5),
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _lib.raise_for(rc)
+    return out
+
+
+SPLIT_CASES = [
+    # B, Sq, Sk, H, D, seed, mask, expected kernel
+    (1, 2048, 1500, 3, 128, 160, None, "flash_fwd_split_kernel<0, 128, 4>"),          # every item split
+    (2, 700, 2100, 2, 128, 161, ("kv_len", 0, 2100), "flash_fwd_split_kernel<0, 128, 4>"),
+    (1, 900, 1100, 3, 64, 162, ("tail_pad", 0, 200), "flash_fwd_split_kernel<1, 64, 4>"),
+    (1, 8192, 2048, 25, 128, 163, None, "flash_fwd_split_kernel<0, 128, 8>"),         # 800 items: 32 split
+]
+
+
+@pytest.mark.parametrize("B,Sq,Sk,H,D,seed,mask,name", SPLIT_CASES)
+def test_flash_key_split(gpu, B, Sq, Sk, H, D, seed, mask, name):
+    """Query tiles of the grid's last round split over the two key halves
+    (fp32 partials merged by a second kernel) against the oracle, and
+    against the unsplit kernel on the same inputs."""
+    from vidax_amd import _lib, flash_attention
+    _say(f"flash key split B={B} Sq={Sq} Sk={Sk} H={H} D={D} mask={mask}")
+    q, k, v, extra = O.make_flash_inputs(B, Sq, Sk, H, D, seed, mask)
+    kw = {key: torch.from_numpy(val).to(gpu) for key, val in extra.items()}
+    if mask is not None and mask[0] == "kv_len":
+        kw["kv_len"][0] = 700          # item 0 has no key in the second half (keys >= 1024)
+        extra["kv_len"][0] = 700
+    tq, tk, tv = _t(q, gpu), _t(k, gpu), _t(v, gpu)
+    out = flash_attention(tq, tk, tv, **kw)
+    assert _lib.last_launch() == name, _lib.last_launch()
+    plain = _plain_flash(tq, tk, tv, kw)
+    torch.cuda.synchronize()
+    rows = _rows(Sq, min(Sq, 256), seed) if Sq > 2048 else np.arange(Sq)
+    ref = O.attention(q[:, rows], k, v, kv_len=extra.get("kv_len"), key_valid=extra.get("key_valid"))
+    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, "split vs oracle")
+    d = (out.float() - plain.float()).abs()
+    print(f"  split vs unsplit: max {d.max().item():.3e} mean {d.mean().item():.3e}", flush=True)
+    assert d.max().item() <= MAX_ABS and d.mean().item() <= MEAN_ABS
+
+
+def test_flash_key_split_key_bias(gpu):
+    """Key split with an additive key bias (-inf runs in both halves): each
+    half starts its accumulators from its own first tile's bias."""
+    from vidax_amd import _lib, flash_attention
+    _say("flash key split + key_bias")
+    B, Sq, Sk, H, D = 1, 1024, 1800, 4, 128
+    q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, D, 170)
+    rng = np.random.default_rng(171)
+    bias = (4.0 * rng.standard_normal((B, Sk))).astype(np.float32)
+    bias[:, 100:300] = -np.inf
+    bias[:, 1200:1250] = -np.inf
+    tq, tk, tv = _t(q, gpu), _t(k, gpu), _t(v, gpu)
+    kb = torch.from_numpy(bias).to(gpu)
+    out = flash_attention(tq, tk, tv, key_bias=kb)
+    assert _lib.last_launch() == "flash_fwd_split_kernel<2, 128, 4>", _lib.last_launch()
+    plain = _plain_flash(tq, tk, tv, {"key_bias": kb})
+    torch.cuda.synchronize()
+    _check(out, O.attention(q, k, v, key_bias=bias), "split key_bias vs oracle")
+    d = (out.float() - plain.float()).abs()
+    print(f"  split vs unsplit: max {d.max().item():.3e} mean {d.mean().item():.3e}", flush=True)
+    assert d.max().item() <= MAX_ABS and d.mean().item() <= MEAN_ABS

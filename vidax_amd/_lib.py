@@ -38,6 +38,9 @@ EXPORTED_SYMBOLS = (
     "vx_last_launch",
     "vx_na3d_qprep_fwd",
     "vx_na3d_qprep_check",
+    "vx_flash_attn_ws_fwd",
+    "vx_flash_attn_workspace_size",
+    "vx_flash_attn_split_plan",
 )
 
 _lock = threading.Lock()
@@ -115,6 +118,13 @@ def lib() -> ctypes.CDLL:
             h.vx_na3d_qprep_fwd.argtypes = _NA3D_QPREP_ARGS + [_p]
             h.vx_na3d_qprep_check.restype = _i32
             h.vx_na3d_qprep_check.argtypes = _NA3D_QPREP_ARGS
+            h.vx_flash_attn_ws_fwd.restype = _i32
+            h.vx_flash_attn_ws_fwd.argtypes = _FLASH_ARGS + [_p, _i64, _p]
+            h.vx_flash_attn_workspace_size.restype = _i64
+            h.vx_flash_attn_workspace_size.argtypes = [_i32] * 5
+            h.vx_flash_attn_split_plan.restype = _i32
+            h.vx_flash_attn_split_plan.argtypes = [_i32] * 6 + [ctypes.POINTER(_i32), ctypes.POINTER(_i32),
+                                                               ctypes.POINTER(_i64)]
             h.vx_last_launch.restype = ctypes.c_char_p
             h.vx_last_launch.argtypes = []
             _lib = h

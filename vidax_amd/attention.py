@@ -169,7 +169,12 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         _lib.raise_for(rc)
         return out
     with torch.cuda.device(dev):
-        rc = L.vx_flash_attn_fwd(
+        # grids whose last round would leave the device mostly idle split
+        # that round's query tiles over two key halves (fp32 partials in a
+        # workspace from torch's caching allocator)
+        ws_bytes = int(L.vx_flash_attn_workspace_size(B, Sq, Sk, H, D))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+        rc = L.vx_flash_attn_ws_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
             kv_len_t.data_ptr() if kv_len_t is not None else None,
             key_valid_t.data_ptr() if key_valid_t is not None else None,
@@ -177,7 +182,8 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
             stride, B, Sq, Sk, H, D,
             _lib.strides3(q.stride()[:3]), _lib.strides3(k.stride()[:3]),
             _lib.strides3(v.stride()[:3]), _lib.strides3(out.stride()[:3]),
-            ctypes.c_float(scale), ctypes.c_void_p(stream))
+            ctypes.c_float(scale), ws.data_ptr() if ws is not None else None, ws_bytes,
+            ctypes.c_void_p(stream))
     _lib.raise_for(rc)
     return out
 

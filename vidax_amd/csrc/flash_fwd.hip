@@ -91,9 +91,14 @@ constexpr float kNegBig = -1.0e30f;           // finite "no key seen yet" max
 
 typedef VX_LDS unsigned char lds_u8;
 
+// One workgroup's work: query tile `qtile` of (head, b) over the keys
+// [k_lo, k_hi) (k_lo a multiple of the key tile). part < 0 writes the
+// normalised bf16 output rows; part >= 0 writes the unnormalised fp32
+// accumulators, the reference point and the row sums to partial slot `part`
+// of a.ws (a key-split item, merged by flash_combine_kernel).
 template <int MASK, int D, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void flash_fwd_kernel(const FlashArgs a) {
+__device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, const int head, const int b,
+                                           const int k_lo, const int k_hi, const int part) {
   using C = FCfg<D, WAVES>;
   constexpr int kWaves = C::kWaves, kThreads = C::kThreads, kNB = C::kNB;
   constexpr int kTileBytes = C::kTileBytes, kVBuf = C::kVBuf, kKBuf = C::kKBuf;
@@ -110,19 +115,18 @@ void flash_fwd_kernel(const FlashArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int hf = lane >> 5;   // which half of the wave
   const int col = lane & 31;  // query column within the wave's 32
-  const int b = blockIdx.z;
-  const int head = blockIdx.y;
-  const int qw0 = (blockIdx.x * kWaves + wave) * 32;
+  const int qw0 = (qtile * kWaves + wave) * 32;
 
   const bf16* qg = (const bf16*)a.q + b * a.qs[0] + head * a.qs[2];
   const bf16* kg = (const bf16*)a.k + b * a.ks[0] + head * a.ks[2];
   const bf16* vg = (const bf16*)a.v + b * a.vs[0] + head * a.vs[2];
   bf16* og = (bf16*)a.o + b * a.os[0] + head * a.os[2];
 
-  int kv_end = a.Sk;
-  if (a.kv_len != nullptr) kv_end = min(max(a.kv_len[b], 0), a.Sk);
+  int kv_end = k_hi;
+  if (a.kv_len != nullptr) kv_end = min(max(a.kv_len[b], 0), k_hi);
   kv_end = __builtin_amdgcn_readfirstlane(kv_end);  // uniform: scalar loop control
-  const int n_tiles = (kv_end + kBN - 1) / kBN;
+  const int t_begin = k_lo / kBN;                   // first key tile of the range
+  const int n_tiles = (kv_end + kBN - 1) / kBN;     // one past the last key tile
   const float c = a.scale * kLog2e;
 
   // ---- Q (B operand of S^T = K Q^T), resident for the whole key loop.
@@ -236,8 +240,8 @@ void flash_fwd_kernel(const FlashArgs a) {
       S[1] = f32x16{};
     }
   };
-  auto qk = [&](int buf_off, f32x16 (&S)[2]) {
-    acc_init(0, S);
+  auto qk = [&](int tile, int buf_off, f32x16 (&S)[2]) {
+    acc_init(tile, S);
     const lds_u8* kb0 = lds + buf_off;
 #pragma unroll
     for (int ds = 0; ds < kDS; ++ds) {
@@ -316,7 +320,7 @@ void flash_fwd_kernel(const FlashArgs a) {
       wait_vmem<(kNB - 2) * 2 * kLoadsPerWave>();
   };
 
-  if (n_tiles > 0) {
+  if (n_tiles > t_begin) {
     // Tile j of K lives in K buffer j % kNB and tile j of V in V buffer
     // j % kNB; V buffer kNB-1 stands in for "V_{-1}" (zeros, paired with P = 0
     // in iteration 0). Iteration t issues K_{t+kNB}, its mask and
@@ -325,9 +329,9 @@ void flash_fwd_kernel(const FlashArgs a) {
     // that every wait below counts whole groups.
 #pragma unroll
     for (int j = 0; j < kNB; ++j) {
-      if (wave < kCopyWaves) stage_k(min(j, n_tiles - 1), kKBuf + j * kTileBytes);
-      stage_mask(min(j, n_tiles - 1));
-      if (j >= 2 && wave < kCopyWaves) stage_v(min(j - 2, n_tiles - 1), kVBuf + (j - 2) * kTileBytes);
+      if (wave < kCopyWaves) stage_k(min(t_begin + j, n_tiles - 1), kKBuf + j * kTileBytes);
+      stage_mask(min(t_begin + j, n_tiles - 1));
+      if (j >= 2 && wave < kCopyWaves) stage_v(min(t_begin + j - 2, n_tiles - 1), kVBuf + (j - 2) * kTileBytes);
     }
 #pragma unroll
     for (int p = 0; p < kTileBytes / (kThreads * 16); ++p)
@@ -344,7 +348,7 @@ void flash_fwd_kernel(const FlashArgs a) {
     }
     __syncthreads();
     f32x16 S[2];
-    qk(kKBuf, S);
+    qk(t_begin, kKBuf, S);
     bf16x8 Pp[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -532,7 +536,7 @@ void flash_fwd_kernel(const FlashArgs a) {
     f32x16 S2[2];
     bf16x8 P2[2][2];
     auto key_loop = [&](auto copy_tag) __attribute__((always_inline)) {
-      int t = 0;
+      int t = t_begin;
       for (; t + 1 < n_tiles; t += 2) {
         step(copy_tag, t, S, S2, Pp, P2);
         step(copy_tag, t + 1, S2, S, P2, Pp);
@@ -555,6 +559,22 @@ void flash_fwd_kernel(const FlashArgs a) {
     pv(kVBuf + vb_prev * kTileBytes, Pp, O);
   }
 
+  // ---- key-split item: the unnormalised accumulators, the reference point
+  // and this lane's part of the row sum go to partial slot `part` (lane
+  // order, one 1 KiB wave store per 16 bytes of each lane).
+  if (part >= 0) {
+    f32x4* slot = (f32x4*)(a.ws + (int64_t)part * flash_part_floats(kWaves, D));
+    f32x4* wo = slot + (int64_t)wave * (kDB * 4) * 64 + lane;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+#pragma unroll
+      for (int k4 = 0; k4 < 4; ++k4)
+        wo[(db * 4 + k4) * 64] = f32x4{O[db][4 * k4], O[db][4 * k4 + 1], O[db][4 * k4 + 2], O[db][4 * k4 + 3]};
+    float* ml = (float*)(slot + (int64_t)kWaves * kDB * 4 * 64) + 2 * (wave * 64 + lane);
+    *(float2*)ml = float2{m_run, l_run};
+    return;
+  }
+
   // ---- epilogue: normalise, pack to 16-byte chunks of 8 consecutive d
   // (pack_out_rows) and store.
   const float lt = halves_sum(l_run);
@@ -571,6 +591,74 @@ void flash_fwd_kernel(const FlashArgs a) {
   }
 }
 
+template <int MASK, int D, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void flash_fwd_kernel(const FlashArgs a) {
+  flash_tile<MASK, D, WAVES>(a, blockIdx.x, blockIdx.y, blockIdx.z, 0, a.Sk, -1);
+}
+
+// Key-split launch: items (query tile fastest, then head, then batch item)
+// below n_full run whole; each of the last a.split_items items runs as two
+// workgroups, over keys [0, k_mid) and [k_mid, Sk), writing partials.
+template <int MASK, int D, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void flash_fwd_split_kernel(const FlashArgs a, int n_full, int n_qt) {
+  const int w = blockIdx.x;
+  int item = w, k_lo = 0, k_hi = a.Sk, part = -1;
+  if (w >= n_full) {
+    part = w - n_full;
+    item = n_full + (part >> 1);
+    if (part & 1)
+      k_lo = a.k_mid;
+    else
+      k_hi = a.k_mid;
+  }
+  const int qt = item % n_qt, bh = item / n_qt;
+  flash_tile<MASK, D, WAVES>(a, qt, bh % a.H, bh / a.H, k_lo, k_hi, part);
+}
+
+// Merges the two key halves of each split item: with M the larger reference
+// point, O = (O0 2^(m0-M) + O1 2^(m1-M)) / (l0 2^(m0-M) + l1 2^(m1-M)),
+// packed and stored as the main kernel's epilogue does (same lane layout).
+template <int D, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void flash_combine_kernel(const FlashArgs a, int n_full, int n_qt) {
+  constexpr int kDB = D / 32;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int hf = lane >> 5, col = lane & 31;
+  const int item = n_full + blockIdx.x;
+  const int qt = item % n_qt, bh = item / n_qt, head = bh % a.H, b = bh / a.H;
+  const f32x4* s0 = (const f32x4*)(a.ws + (int64_t)(2 * blockIdx.x) * flash_part_floats(WAVES, D));
+  const f32x4* s1 = (const f32x4*)(a.ws + (int64_t)(2 * blockIdx.x + 1) * flash_part_floats(WAVES, D));
+  const int ml_idx = 2 * (wave * 64 + lane);
+  const float2 ml0 = *(const float2*)((const float*)(s0 + (int64_t)WAVES * kDB * 4 * 64) + ml_idx);
+  const float2 ml1 = *(const float2*)((const float*)(s1 + (int64_t)WAVES * kDB * 4 * 64) + ml_idx);
+  const float M = fmaxf(ml0.x, ml1.x);
+  const float a0 = fast_exp2(ml0.x - M), a1 = fast_exp2(ml1.x - M);
+  const float lt = halves_sum(ml0.y * a0 + ml1.y * a1);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  f32x16 O[kDB];
+  const int64_t base = (int64_t)wave * (kDB * 4) * 64 + lane;
+#pragma unroll
+  for (int db = 0; db < kDB; ++db)
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) {
+      const f32x4 x0 = s0[base + (db * 4 + k4) * 64], x1 = s1[base + (db * 4 + k4) * 64];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) O[db][4 * k4 + e] = x0[e] * a0 + x1[e] * a1;
+    }
+  u32x4 chunk[kDB][2];
+  pack_out_rows<kDB>(O, inv, chunk);
+  const int qi = (qt * WAVES + wave) * 32 + col;
+  if (qi < a.Sq) {
+    bf16* orow = (bf16*)a.o + b * a.os[0] + head * a.os[2] + (int64_t)qi * a.os[1];
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) *(u32x4*)(orow + db * 32 + (2 * pr + hf) * 8) = chunk[db][pr];
+  }
+}
+
 // Name of a flash_fwd_kernel instantiation, as the profiler prints it.
 template <int MASK, int D, int WAVES>
 const char* flash_kernel_name() {
@@ -579,9 +667,29 @@ const char* flash_kernel_name() {
   return name.c_str();
 }
 
+template <int MASK, int D, int WAVES>
+const char* flash_split_kernel_name() {
+  static const std::string name = "flash_fwd_split_kernel<" + std::to_string(MASK) + ", " + std::to_string(D) +
+                                  ", " + std::to_string(WAVES) + ">";
+  return name.c_str();
+}
+
 template <int MASK, int WAVES, int D>
 int launch_one(const FlashArgs& a, hipStream_t stream, const char** launched) {
-  dim3 grid((a.Sq + WAVES * 32 - 1) / (WAVES * 32), a.H, a.B);
+  const int n_qt = (a.Sq + WAVES * 32 - 1) / (WAVES * 32);
+  if constexpr (!(MASK & kMaskFull)) {  // the per-(query, key) bias path is not split
+    if (a.split_items > 0) {
+    const int n_items = n_qt * a.H * a.B;
+    const int n_full = n_items - a.split_items;
+    hipLaunchKernelGGL((flash_fwd_split_kernel<MASK, D, WAVES>), dim3(n_full + 2 * a.split_items),
+                       dim3(WAVES * 64), 0, stream, a, n_full, n_qt);
+    hipLaunchKernelGGL((flash_combine_kernel<D, WAVES>), dim3(a.split_items), dim3(WAVES * 64), 0, stream, a,
+                       n_full, n_qt);
+    *launched = flash_split_kernel_name<MASK, D, WAVES>();
+    return (int)hipGetLastError();
+    }
+  }
+  dim3 grid(n_qt, a.H, a.B);
   hipLaunchKernelGGL((flash_fwd_kernel<MASK, D, WAVES>), grid, dim3(WAVES * 64), 0, stream, a);
   *launched = flash_kernel_name<MASK, D, WAVES>();
   return (int)hipGetLastError();
@@ -596,6 +704,18 @@ int launch(const FlashArgs& a, hipStream_t stream, const char** launched) {
 }
 
 }  // namespace
+
+int device_cu_count() {
+  static int counts[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (counts[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    counts[dev] = n;
+  }
+  return counts[dev];
+}
 
 int launch_flash_fwd(const FlashArgs& a, void* stream, const char** launched) {
   if (a.D != 128 && a.D != 64) return (int)hipErrorNotSupported;

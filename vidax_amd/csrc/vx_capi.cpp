@@ -149,6 +149,39 @@ void flash_kernel_label(int32_t mask_kind, int32_t D, int32_t waves, char* out, 
   if (out != nullptr && len > 0) snprintf(out, (size_t)len, "flash_fwd_kernel<%d, %d, %d>", mask_kind, D, waves);
 }
 
+// ---- key split of the last round of a grid (vx_flash_attn_ws_fwd).
+//
+// A grid of n_items (query tile, head, batch) workgroups over `slots`
+// resident workgroups (two 4-wave or one 8-wave workgroup per compute unit)
+// runs ceil(n_items / slots) rounds; when the last round holds r <= slots/2
+// items, running each of those as two workgroups over half the keys (and
+// merging the halves) makes that round take half as long. Key sequences
+// shorter than kMinSplitTiles key tiles are not split.
+constexpr int32_t kMinSplitTiles = 16;
+
+struct SplitPlan {
+  int32_t items = 0;  // items split in two (0: none)
+  int32_t k_mid = 0;  // first key of the second half (a multiple of the key tile)
+  int64_t ws_bytes = 0;
+};
+
+SplitPlan flash_split_plan(int32_t B, int32_t Sq, int32_t Sk, int32_t H, int32_t D, int32_t waves,
+                           int32_t num_cus) {
+  SplitPlan p;
+  const int64_t tiles = ((int64_t)Sk + kKeyTile - 1) / kKeyTile;
+  if (num_cus <= 0 || tiles < kMinSplitTiles) return p;
+  const int64_t n_qt = ((int64_t)Sq + waves * 32 - 1) / (waves * 32);
+  const int64_t n_items = n_qt * H * B;
+  const int64_t slots = (int64_t)num_cus * (waves == 4 ? 2 : 1);
+  const int64_t rounds = (n_items + slots - 1) / slots;
+  const int64_t r = n_items - (rounds - 1) * slots;
+  if (r > slots / 2 || r > (1 << 20)) return p;
+  p.items = (int32_t)r;
+  p.k_mid = (int32_t)(tiles / 2 * kKeyTile);
+  p.ws_bytes = 2 * r * vx::flash_part_floats(waves, D) * (int64_t)sizeof(float);
+  return p;
+}
+
 // ---- neighbourhood-attention launch plan, by the clamped x window.
 int32_t na3d_variant(int32_t kw_clamped, int32_t D) {
   if (kw_clamped <= 9) return vx::kNaPipe16;
@@ -228,6 +261,9 @@ int32_t flash_check(const void* q, const void* k, const void* v, const void* out
   if ((rc = flash_plan(B, Sq, Sk, H, &waves)) != VX_OK) return rc;
   if (args != nullptr) {
     args->waves = waves;
+    args->split_items = 0;
+    args->k_mid = 0;
+    args->ws = nullptr;
     args->q = q;
     args->k = k;
     args->v = v;
@@ -425,6 +461,59 @@ const char* vx_last_error(void) { return g_error; }
 void vx_debug_inject_error(int32_t code) { g_inject.store(code, std::memory_order_relaxed); }
 
 const char* vx_last_launch(void) { return g_last_launch; }
+
+int32_t vx_flash_attn_split_plan(int32_t batch, int32_t seq_q, int32_t seq_k, int32_t num_heads, int32_t head_dim,
+                                 int32_t num_cus, int32_t* split_items, int32_t* split_key,
+                                 int64_t* workspace_bytes) {
+  if (batch < 1 || seq_q < 1 || seq_k < 1 || num_heads < 1)
+    return fail(VX_ERR_INVALID_ARGUMENT, "batch, seq_q, seq_k and num_heads must be >= 1");
+  if (head_dim != 128 && head_dim != 64)
+    return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 64 and 128)", head_dim);
+  int32_t waves = 0;
+  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, &waves);
+  if (rc != VX_OK) return rc;
+  const SplitPlan p = flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, waves, num_cus);
+  if (split_items != nullptr) *split_items = p.items;
+  if (split_key != nullptr) *split_key = p.k_mid;
+  if (workspace_bytes != nullptr) *workspace_bytes = p.ws_bytes;
+  return ok();
+}
+
+int64_t vx_flash_attn_workspace_size(int32_t batch, int32_t seq_q, int32_t seq_k, int32_t num_heads,
+                                     int32_t head_dim) {
+  int64_t bytes = 0;
+  if (vx_flash_attn_split_plan(batch, seq_q, seq_k, num_heads, head_dim, vx::device_cu_count(), nullptr, nullptr,
+                               &bytes) != VX_OK)
+    return 0;
+  return bytes;
+}
+
+int32_t vx_flash_attn_ws_fwd(const void* q, const void* k, const void* v, void* out, const int32_t* kv_len,
+                             const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride,
+                             int32_t batch, int32_t seq_q, int32_t seq_k, int32_t num_heads, int32_t head_dim,
+                             const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                             const int64_t* out_strides, float scale, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  vx::FlashArgs args;
+  int32_t rc = flash_check(q, k, v, out, kv_len, key_valid, key_bias, key_mask_stride, batch, seq_q, seq_k,
+                           num_heads, head_dim, q_strides, k_strides, v_strides, out_strides, scale, &args);
+  if (rc != VX_OK) return rc;
+  if (workspace_bytes < 0) return fail(VX_ERR_INVALID_ARGUMENT, "workspace_bytes must be >= 0");
+  if (workspace != nullptr && !aligned16(workspace))
+    return fail(VX_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  if ((rc = injected()) != VX_OK) return rc;
+  const SplitPlan p = flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, args.waves, vx::device_cu_count());
+  if (p.items > 0 && workspace != nullptr && workspace_bytes >= p.ws_bytes) {
+    args.split_items = p.items;
+    args.k_mid = p.k_mid;
+    args.ws = static_cast<float*>(workspace);
+  }
+  const char* launched = "";
+  const int err = vx::launch_flash_fwd(args, stream, &launched);
+  if (err != 0) return fail(VX_ERR_LAUNCH, "flash attention launch failed (hipError_t %d)", err);
+  g_last_launch = launched;
+  return ok();
+}
 
 int32_t vx_flash_attn_plan(int32_t batch, int32_t seq_q, int32_t seq_k, int32_t num_heads, int32_t head_dim,
                            int32_t mask_kind, char* kernel_name, int32_t name_len) {

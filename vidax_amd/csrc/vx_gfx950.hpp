@@ -159,11 +159,11 @@ __device__ __forceinline__ uint64_t uniform_u64(uint64_t x) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-// raw_rsrc from a wave-uniform byte address.
+// raw_rsrc from a wave-uniform byte address (kept in scalar registers).
 __device__ __forceinline__ i32x4_rsrc raw_rsrc_u64(uint64_t addr) {
   i32x4_rsrc r;
-  r[0] = (int)(uint32_t)addr;
-  r[1] = (int)(uint32_t)(addr >> 32);
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
+  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(addr >> 32));
   r[2] = -1;
   r[3] = 0x00020000;
   return r;

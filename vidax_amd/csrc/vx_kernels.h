@@ -24,7 +24,20 @@ struct FlashArgs {
   int64_t qs[3], ks[3], vs[3], os[3];
   float scale;  // softmax scale (> 0)
   int32_t waves;  // workgroup size chosen by the launch plan: 4 (128 queries) or 8 (256)
+  // Key split chosen by the launch plan (split_items = 0: none): each of the
+  // last split_items (query tile, head, batch) items runs as two workgroups
+  // over keys [0, k_mid) and [k_mid, Sk), writing fp32 partials to ws
+  // (flash_part_floats floats per workgroup), merged by a second kernel.
+  int32_t split_items;
+  int32_t k_mid;
+  float* ws;
 };
+
+// fp32 values of one key-split partial: the lanes' O accumulators, then
+// (reference point, row sum) per lane.
+constexpr int64_t flash_part_floats(int waves, int head_dim) {
+  return (int64_t)waves * 64 * ((head_dim / 32) * 16 + 2);
+}
 
 // Neighbourhood attention launch arguments; tensors are contiguous
 // (B, T, Hs, W, NH, D).
@@ -72,6 +85,9 @@ struct PrologueArgs {
   int32_t B, S, H, D;
   int64_t x_bstride, x_sstride, o_bstride, o_sstride, tab_stride;  // elements
 };
+
+// Compute units of the current device (0 if unknown), cached per device.
+int device_cu_count();
 
 // All return a hipError_t value (0 on success) and store the name of the kernel they launched in *launched (a string with
 // static storage, built from the launched instantiation's template
