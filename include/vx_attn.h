@@ -99,6 +99,24 @@ int32_t vx_flash_attn_ws_fwd(const void* q, const void* k, const void* v, void* 
                              void* stream);
 
 /*
+ * vx_flash_attn_ws_fwd for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation):
+ * the same arguments as vx_flash_attn_fwd, and the key split's partials
+ * go to a static device array of the library (36 MiB per device, held
+ * until the process ends) instead of a workspace. The call allocates
+ * nothing. A shape whose split needs more than that scratch fails with
+ * VX_ERR_UNSUPPORTED (no MI355X shape does: the plan uses at most 33 MiB).
+ * Calls on one device share the scratch: calls that overlap on one device
+ * (different streams, or host threads) race and must be serialised by the
+ * caller. No counterpart in the reference: it exists for the callers above.
+ */
+int32_t vx_flash_attn_noalloc_fwd(const void* q, const void* k, const void* v, void* out, const int32_t* kv_len,
+                                  const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride,
+                                  int32_t batch, int32_t seq_q, int32_t seq_k, int32_t num_heads, int32_t head_dim,
+                                  const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                                  const int64_t* out_strides, float scale, void* stream);
+
+/*
  * Workspace bytes vx_flash_attn_ws_fwd uses for this shape on the current
  * device (0 when it does not split, or on failure). Head dim 64 or 128.
  */

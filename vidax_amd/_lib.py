@@ -41,6 +41,7 @@ EXPORTED_SYMBOLS = (
     "vx_flash_attn_ws_fwd",
     "vx_flash_attn_workspace_size",
     "vx_flash_attn_split_plan",
+    "vx_flash_attn_noalloc_fwd",
 )
 
 _lock = threading.Lock()
@@ -120,6 +121,8 @@ def lib() -> ctypes.CDLL:
             h.vx_na3d_qprep_check.argtypes = _NA3D_QPREP_ARGS
             h.vx_flash_attn_ws_fwd.restype = _i32
             h.vx_flash_attn_ws_fwd.argtypes = _FLASH_ARGS + [_p, _i64, _p]
+            h.vx_flash_attn_noalloc_fwd.restype = _i32
+            h.vx_flash_attn_noalloc_fwd.argtypes = _FLASH_ARGS + [_p]
             h.vx_flash_attn_workspace_size.restype = _i64
             h.vx_flash_attn_workspace_size.argtypes = [_i32] * 5
             h.vx_flash_attn_split_plan.restype = _i32

@@ -33,6 +33,7 @@
 #include "vx_gfx950.hpp"
 #include "vx_kernels.h"
 
+#include <mutex>
 #include <string>
 
 namespace vx {
@@ -704,6 +705,37 @@ int launch(const FlashArgs& a, hipStream_t stream, const char** launched) {
 }
 
 }  // namespace
+
+// ---- scratch of the allocation-free entry point (vx_flash_attn_noalloc_fwd):
+// the key-split partials live in this file-scope device array instead of a
+// workspace. Each device that runs the library holds one copy until the
+// process ends; calls on one device share it (their split launches must not
+// overlap). kNoallocScratchBytes covers every split plan of a device with up
+// to 262 compute units (the plan uses at most one partial slot per resident
+// workgroup: 2 x 256 x 4 waves x 64 lanes x 66 floats = 33 MiB on MI355X).
+constexpr int64_t kNoallocScratchBytes = 36ll << 20;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+int noalloc_scratch(void** ptr, int64_t* bytes) {
+  // device address of `scratch`, looked up once per device with that device
+  // current (the host-side name is only a handle for the lookup)
+  static std::mutex mu;
+  static void* addr[64] = {nullptr};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= 64) return (int)hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    addr[dev] = p;
+  }
+  *ptr = addr[dev];
+  *bytes = kNoallocScratchBytes;
+  return 0;
+}
 
 int device_cu_count() {
   static int counts[64] = {0};

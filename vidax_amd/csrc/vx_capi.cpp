@@ -572,6 +572,38 @@ int32_t vx_flash_attn_fwd(const void* q, const void* k, const void* v, void* out
   return ok();
 }
 
+int32_t vx_flash_attn_noalloc_fwd(const void* q, const void* k, const void* v, void* out, const int32_t* kv_len,
+                                  const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride,
+                                  int32_t batch, int32_t seq_q, int32_t seq_k, int32_t num_heads, int32_t head_dim,
+                                  const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                                  const int64_t* out_strides, float scale, void* stream) {
+  vx::FlashArgs args;
+  int32_t rc = flash_check(q, k, v, out, kv_len, key_valid, key_bias, key_mask_stride, batch, seq_q, seq_k,
+                           num_heads, head_dim, q_strides, k_strides, v_strides, out_strides, scale, &args);
+  if (rc != VX_OK) return rc;
+  if ((rc = injected()) != VX_OK) return rc;
+  const SplitPlan p = flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, args.waves, vx::device_cu_count());
+  if (p.items > 0) {
+    void* ws = nullptr;
+    int64_t cap = 0;
+    const int err = vx::noalloc_scratch(&ws, &cap);
+    if (err != 0) return fail(VX_ERR_LAUNCH, "looking up the static scratch failed (hipError_t %d)", err);
+    if (p.ws_bytes > cap)
+      return fail(VX_ERR_UNSUPPORTED,
+                  "this shape splits its keys over %lld bytes of scratch; the static scratch holds %lld "
+                  "(use vx_flash_attn_ws_fwd with a workspace)",
+                  (long long)p.ws_bytes, (long long)cap);
+    args.split_items = p.items;
+    args.k_mid = p.k_mid;
+    args.ws = static_cast<float*>(ws);
+  }
+  const char* launched = "";
+  const int err = vx::launch_flash_fwd(args, stream, &launched);
+  if (err != 0) return fail(VX_ERR_LAUNCH, "flash attention launch failed (hipError_t %d)", err);
+  g_last_launch = launched;
+  return ok();
+}
+
 int32_t vx_flash_attn_bias_check(const void* q, const void* k, const void* v, const void* out, const int32_t* kv_len,
                                  const uint8_t* key_valid, const float* key_bias, int64_t key_mask_stride,
                                  const float* bias, const int64_t* bias_strides, int32_t batch, int32_t seq_q,

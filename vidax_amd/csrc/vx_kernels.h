@@ -89,6 +89,10 @@ struct PrologueArgs {
 // Compute units of the current device (0 if unknown), cached per device.
 int device_cu_count();
 
+// Device address and size of the current device's static scratch array
+// (used by vx_flash_attn_noalloc_fwd); returns a hipError_t value.
+int noalloc_scratch(void** ptr, int64_t* bytes);
+
 // All return a hipError_t value (0 on success) and store the name of the kernel they launched in *launched (a string with
 // static storage, built from the launched instantiation's template
 // arguments).
