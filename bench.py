@@ -36,6 +36,12 @@ WORKLOADS = {
                             "cross-attention B=2 H=40 Lq=32760 Lk=512, kv_len ~ U{20..512}"),
     "joint_L119056_H24": ("flash", dict(B=1, Sq=119056, Sk=119056, H=24, seed=4, tail_pad=(0, 200)),
                           "joint self-attention B=1 H=24 S=33*45*80+256, last 0-200 keys masked"),
+    "self_key_bias_L32760_H40": ("flash", dict(B=1, Sq=32760, Sk=32760, H=40, seed=1, key_bias_pad=(100, 300)),
+                                 "self-attention B=1 H=40 L=32760 D=128 with a (B,1,1,Sk) additive key bias, "
+                                 "-inf on a mid-sequence run of 100-300 keys (Cosmos3 text padding)"),
+    "t5_rel_bias_L512_H8_D64": ("flash", dict(B=2, Sq=512, Sk=512, H=8, D=64, seed=7, scale=1.0, t5_bias=True),
+                                "UMT5 encoder attention B=2 L=512 H=8 D=64, scale 1, (1,H,L,L) relative-position "
+                                "bias + (B,1,1,L) padding mask"),
     "na3d_21x45x80_H24": ("na3d", dict(B=1, T=21, Hs=45, W=80, NH=24, kernel=(3, 7, 7), seed=3),
                           "3D neighbourhood attention 21x45x80, window (3,7,7), B=1 NH=24 D=128"),
     "na3d_stage5_33x88x160_H4_D64": ("na3d", dict(B=1, T=33, Hs=88, W=160, NH=4, D=64, kernel=(11, 11, 11),
@@ -70,10 +76,10 @@ def _flash_inputs(p, dev):
     import torch
     g = torch.Generator(device=dev)
     g.manual_seed(p["seed"])
-    B, Sq, Sk, H = p["B"], p["Sq"], p["Sk"], p["H"]
-    q = torch.randn((B, Sq, H, 128), generator=g, device=dev).to(torch.bfloat16)
-    k = torch.randn((B, Sk, H, 128), generator=g, device=dev).to(torch.bfloat16)
-    v = torch.randn((B, Sk, H, 128), generator=g, device=dev).to(torch.bfloat16)
+    B, Sq, Sk, H, D = p["B"], p["Sq"], p["Sk"], p["H"], p.get("D", 128)
+    q = torch.randn((B, Sq, H, D), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((B, Sk, H, D), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((B, Sk, H, D), generator=g, device=dev).to(torch.bfloat16)
     kw = {}
     valid_keys = [Sk] * B
     rng = np.random.default_rng(p["seed"])
@@ -93,14 +99,34 @@ def _flash_inputs(p, dev):
         from vidax_amd.attention import _last_valid_plus_one
         kw["kv_len"] = _last_valid_plus_one(valid)
         valid_keys = [Sk - int(x) for x in pad]
+    if "key_bias_pad" in p:
+        lo, hi = p["key_bias_pad"]
+        n_pad = int(rng.integers(lo, hi + 1))
+        bias = torch.randn((B, Sk), generator=g, device=dev)
+        s0 = Sk // 3
+        bias[:, s0:s0 + n_pad] = float("-inf")
+        kw["key_bias"] = bias
+        valid_keys = [Sk - n_pad] * B
+    if p.get("t5_bias"):
+        # learned relative-position bias (1, H, L, L) plus a padding mask: the
+        # second batch item's last 200 keys are padding
+        bias = torch.randn((1, H, Sq, Sk), generator=g, device=dev)
+        pad = torch.zeros((B, 1, 1, Sk), device=dev)
+        pad[1, ..., Sk - 200:] = float("-inf")
+        kw["bias"] = bias + pad
+        kw["scale"] = p.get("scale", 1.0)
+        valid_keys = [Sk, Sk - 200]
     return q, k, v, kw, valid_keys
 
 
 def _flash_work(p, valid_keys):
-    """Algorithmic flops and HBM bytes per call (q, o and the valid k, v once)."""
-    H, D, Sq = p["H"], 128, p["Sq"]
+    """Algorithmic flops and HBM bytes per call (q, o and the valid k, v once,
+    plus a per-(query, key) bias once)."""
+    H, D, Sq = p["H"], p.get("D", 128), p["Sq"]
     flops = 4.0 * H * D * Sq * sum(valid_keys)
     bytes_ = 2.0 * (p["B"] * Sq * H * D * 2) + 2.0 * sum(valid_keys) * H * D * 2
+    if p.get("t5_bias"):
+        bytes_ += 4.0 * H * Sq * p["Sk"]
     return flops, bytes_
 
 
@@ -125,11 +151,11 @@ def _cpu_baseline(kind, p, budget_s=12.0):
         threads = os.cpu_count() or 1
     rng = np.random.default_rng(1234)
     if kind == "flash":
-        H, Sk = 1, p["Sk"]
+        H, Sk, D = 1, p["Sk"], p.get("D", 128)
         rows = 1024
-        q = O.bf16_round(rng.standard_normal((1, rows, H, 128), dtype=np.float32))
-        k = O.bf16_round(rng.standard_normal((1, Sk, H, 128), dtype=np.float32))
-        v = O.bf16_round(rng.standard_normal((1, Sk, H, 128), dtype=np.float32))
+        q = O.bf16_round(rng.standard_normal((1, rows, H, D), dtype=np.float32))
+        k = O.bf16_round(rng.standard_normal((1, Sk, H, D), dtype=np.float32))
+        v = O.bf16_round(rng.standard_normal((1, Sk, H, D), dtype=np.float32))
         O.attention(q[:, :64], k, v, acc=np.float32)  # warm-up
         reps, t0 = 0, time.perf_counter()
         while True:
@@ -138,9 +164,9 @@ def _cpu_baseline(kind, p, budget_s=12.0):
             el = time.perf_counter() - t0
             if el >= budget_s or reps >= 1000:
                 break
-        flops = 4.0 * 128 * rows * Sk * H * reps
+        flops = 4.0 * D * rows * Sk * H * reps
         sample = (f"oracle fp32 (numpy/BLAS) attention, {reps} x (1 head x {rows} query rows x "
-                  f"{Sk} keys, D=128) of this workload, {el:.1f} s")
+                  f"{Sk} keys, D={D}) of this workload, {el:.1f} s")
         return {"value": round(flops / el / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads),
                 "kind": "port", "sample": sample}
     if kind == "na3d_block":

@@ -85,8 +85,8 @@ int32_t vx_flash_attn_fwd(const void* q, const void* k, const void* v, void* out
  * workgroups over the two halves of the keys, whose fp32 partial results go
  * to the workspace and are merged by a second kernel on the same stream.
  * That needs vx_flash_attn_workspace_size() bytes (0: no split for this
- * shape on this device); with a smaller workspace (or NULL) the call runs
- * without the split, as vx_flash_attn_fwd. The workspace must be 16-byte
+ * shape on this device); with a smaller workspace (or NULL), or with a
+ * key_bias, the call runs without the split, as vx_flash_attn_fwd. The workspace must be 16-byte
  * aligned and stay untouched until the work on `stream` has finished; calls
  * that overlap on different streams need different workspaces.
  * Replaces the same reference call sites as vx_flash_attn_fwd.
@@ -101,7 +101,8 @@ int32_t vx_flash_attn_ws_fwd(const void* q, const void* k, const void* v, void* 
 /*
  * vx_flash_attn_ws_fwd for callers that cannot allocate (code under HIP
  * graph capture, tight serving loops, harnesses that forbid allocation):
- * the same arguments as vx_flash_attn_fwd, and the key split's partials
+ * the same arguments as vx_flash_attn_fwd (calls with a key_bias do not
+ * split, as in vx_flash_attn_ws_fwd), and the key split's partials
  * go to a static device array of the library (36 MiB per device, held
  * until the process ends) instead of a workspace. The call allocates
  * nothing. A shape whose split needs more than that scratch fails with
@@ -142,7 +143,9 @@ int32_t vx_flash_attn_split_plan(int32_t batch, int32_t seq_q, int32_t seq_k, in
  * (0 broadcasts, e.g. T5's (1, H, L, L) bias over the batch); keys are
  * contiguous and every query row must be readable for round_up(seq_k, 64)
  * elements; bias 16-byte aligned. The bias is read per query row from global
- * memory, which suits the short sequences that use it (text encoders).
+ * memory, which suits the short sequences that use it (text encoders); these
+ * calls always run 128-query workgroups (VIDAX_FLASH_BLOCK_SIZES does not
+ * apply to them).
  *
  * Replaces the reference's non-kernel branch of dot_product_attention for a
  * head- or query-dependent bias or boolean mask:

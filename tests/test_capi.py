@@ -259,6 +259,8 @@ def test_flash_kernel_name_follows_the_launch_rule():
     assert flash_kernel_name(1, 7800, 7800, 12) == "flash_fwd_kernel<0, 128, 4>"      # 372 tiles
     assert flash_kernel_name(2, 32760, 512, 40) == "flash_fwd_kernel<0, 128, 4>"      # short keys
     assert flash_kernel_name(1, 200, 200, 4, 64, 4) == "flash_fwd_kernel<4, 64, 4>"
+    # a per-(query, key) bias always runs 128-query workgroups
+    assert flash_kernel_name(1, 32760, 32760, 40, 128, 5) == "flash_fwd_kernel<5, 128, 4>"
     assert flash_kernel_name(3, 65536, 1025, 1) == "flash_fwd_kernel<0, 128, 8>"      # 768 tiles
 
 

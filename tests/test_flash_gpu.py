@@ -393,7 +393,8 @@ def test_flash_eight_wave_variants(gpu, D, kind):
     from vidax_amd import _lib, dot_product_attention, flash_attention
     B, Sq, Sk, H = 1, 8192, 1100, 24
     mask_kind = {"plain": 0, "kv_len": 0, "key_valid": 1, "key_bias": 2, "all_key_masks": 3, "full_bias": 5}[kind]
-    name = f"flash_fwd_kernel<{mask_kind}, {D}, 8>"
+    # (a per-(query, key) bias always runs 128-query workgroups)
+    name = f"flash_fwd_kernel<{mask_kind}, {D}, {4 if kind == 'full_bias' else 8}>"
     _say(f"flash 8 waves {name} kind={kind} B={B} Sq={Sq} Sk={Sk} H={H} D={D}")
     seed = 90 + EIGHT_WAVE_KINDS.index(kind) + (0 if D == 128 else 10)
     q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, D, seed)
@@ -617,9 +618,9 @@ def test_flash_key_split(gpu, B, Sq, Sk, H, D, seed, mask, name):
     assert d.max().item() <= MAX_ABS and d.mean().item() <= MEAN_ABS
 
 
-def test_flash_key_split_key_bias(gpu):
-    """Key split with an additive key bias (-inf runs in both halves): each
-    half starts its accumulators from its own first tile's bias."""
+def test_flash_key_bias_is_not_split(gpu):
+    """A shape whose grid would split its keys runs unsplit when a key bias is
+    given (-inf runs in both halves of the keys), and matches the oracle."""
     from vidax_amd import _lib, flash_attention
     _say("flash key split + key_bias")
     B, Sq, Sk, H, D = 1, 1024, 1800, 4, 128
@@ -631,7 +632,7 @@ def test_flash_key_split_key_bias(gpu):
     tq, tk, tv = _t(q, gpu), _t(k, gpu), _t(v, gpu)
     kb = torch.from_numpy(bias).to(gpu)
     out = flash_attention(tq, tk, tv, key_bias=kb)
-    assert _lib.last_launch() == "flash_fwd_split_kernel<2, 128, 4>", _lib.last_launch()
+    assert _lib.last_launch() == "flash_fwd_kernel<2, 128, 4>", _lib.last_launch()
     plain = _plain_flash(tq, tk, tv, {"key_bias": kb})
     torch.cuda.synchronize()
     _check(out, O.attention(q, k, v, key_bias=bias), "split key_bias vs oracle")

@@ -121,7 +121,6 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
   const bf16* qg = (const bf16*)a.q + b * a.qs[0] + head * a.qs[2];
   const bf16* kg = (const bf16*)a.k + b * a.ks[0] + head * a.ks[2];
   const bf16* vg = (const bf16*)a.v + b * a.vs[0] + head * a.vs[2];
-  bf16* og = (bf16*)a.o + b * a.os[0] + head * a.os[2];
 
   int kv_end = k_hi;
   if (a.kv_len != nullptr) kv_end = min(max(a.kv_len[b], 0), k_hi);
@@ -175,17 +174,23 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
   // tile (a tile spans 63 rows of the key stride, at most 2^24 elements:
   // well inside 32 bits); each tile's copies go through a buffer resource
   // based at its first row
-  using LaneSrc = uint32_t;
-  LaneSrc klane[kLoadsPerWave];
-  LaneSrc vlane[kLoadsPerWave];
+  // (computed where a copying wave issues copies, so they are not live
+  // in the other waves' key loop)
+  struct Lanes {
+    uint32_t k[kLoadsPerWave], v[kLoadsPerWave];
+  };
+  auto make_lanes = [&]() {
+    Lanes ln;
 #pragma unroll
-  for (int p = 0; p < kLoadsPerWave; ++p) {
-    const int i = (wave % kCopyWaves) * kLoadsPerWave + p;
-    const int r = 8 * (i & 7) + srow;
-    const int col_el = (i >> 3) * 64 + ((scol ^ half_swizzle(r)) * 8);
-    klane[p] = (uint32_t)(r * (int)a.ks[1] + col_el) * 2u;
-    vlane[p] = (uint32_t)(r * (int)a.vs[1] + col_el) * 2u;
-  }
+    for (int p = 0; p < kLoadsPerWave; ++p) {
+      const int i = (wave % kCopyWaves) * kLoadsPerWave + p;
+      const int r = 8 * (i & 7) + srow;
+      const int col_el = (i >> 3) * 64 + ((scol ^ half_swizzle(r)) * 8);
+      ln.k[p] = (uint32_t)(r * (int)a.ks[1] + col_el) * 2u;
+      ln.v[p] = (uint32_t)(r * (int)a.vs[1] + col_el) * 2u;
+    }
+    return ln;
+  };
   // Byte address of this head's first k / v row and the byte distance
   // between consecutive 64-key tiles, in scalar registers: each tile's copies
   // go through one buffer resource based at the tile's first row, formed with
@@ -198,7 +203,7 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
   // (every row below kv_end) issues its copies back to back with per-lane
   // offsets computed once; only the tail tile clamps its rows (one uniform
   // branch per tile and tensor)
-  auto stage = [&](uint64_t addr0, uint64_t tile_bytes, const LaneSrc (&lanep)[kLoadsPerWave], int64_t sstride,
+  auto stage = [&](uint64_t addr0, uint64_t tile_bytes, const uint32_t (&lanep)[kLoadsPerWave], int64_t sstride,
                    int t, int buf_off) {
     const i32x4_rsrc rs = raw_rsrc_u64(addr0 + (uint64_t)t * tile_bytes);
     const uint32_t dst = lds_base + buf_off + (uint32_t)(wave * kLoadsPerWave) * 1024u;
@@ -217,8 +222,8 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
       }
     }
   };
-  auto stage_k = [&](int t, int buf_off) { stage(k_addr, k_tile_bytes, klane, a.ks[1], t, buf_off); };
-  auto stage_v = [&](int t, int buf_off) { stage(v_addr, v_tile_bytes, vlane, a.vs[1], t, buf_off); };
+  auto stage_k = [&](const Lanes& ln, int t, int buf_off) { stage(k_addr, k_tile_bytes, ln.k, a.ks[1], t, buf_off); };
+  auto stage_v = [&](const Lanes& ln, int t, int buf_off) { stage(v_addr, v_tile_bytes, ln.v, a.vs[1], t, buf_off); };
 
   // A per-key bias enters the scores through the QK^T accumulator: it starts
   // at bias / scale for the lane's keys kb*32 + g*8 + hf*4 + 0..3 of tile j
@@ -301,14 +306,18 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
   // Wave 0 stages tile j's mask (64 validity bytes: lanes 0-3; 64 biases:
   // lanes 0-15) into mask slot j % kMaskRing. Mask rows hold whole 64-key
   // tiles.
+  // (buffer form from the batch item's mask row in scalar registers, so the
+  // per-lane part of the source is a small constant offset)
+  const uint64_t vrow_addr = uniform_u64((uint64_t)(uintptr_t)vrow);
+  const uint64_t brow_addr = uniform_u64((uint64_t)(uintptr_t)brow);
   auto stage_mask = [&](int j) {
     if (!MASKED || wave != 0) return;
     const uint32_t slot = lds_base + kMaskBuf + (j & (kMaskRing - 1)) * kMaskSlot;
     if (MASK & kMaskValid) {
-      if (lane < 4) lds_dma16(vrow + j * kBN + lane * 16, slot);
+      if (lane < 4) lds_dma16_buf(raw_rsrc_u64(vrow_addr + (uint64_t)j * kBN), lane * 16, slot);
     }
     if (MASK & kMaskBias) {
-      if (lane < 16) lds_dma16(brow + j * kBN + lane * 4, slot + 64);
+      if (lane < 16) lds_dma16_buf(raw_rsrc_u64(brow_addr + (uint64_t)j * kBN * 4), lane * 16, slot + 64);
     }
   };
   // At the top of iteration t: the tiles it reads (K_{t+1}, V_{t-1}) were
@@ -328,11 +337,14 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
     // V_{t+kNB-2}, into the buffers that the previous iteration finished
     // reading; the prologue issues the same groups for t = -kNB .. -1, so
     // that every wait below counts whole groups.
+    if (wave < kCopyWaves) {
+      const Lanes ln = make_lanes();
 #pragma unroll
-    for (int j = 0; j < kNB; ++j) {
-      if (wave < kCopyWaves) stage_k(min(t_begin + j, n_tiles - 1), kKBuf + j * kTileBytes);
-      stage_mask(min(t_begin + j, n_tiles - 1));
-      if (j >= 2 && wave < kCopyWaves) stage_v(min(t_begin + j - 2, n_tiles - 1), kVBuf + (j - 2) * kTileBytes);
+      for (int j = 0; j < kNB; ++j) {
+        stage_k(ln, min(t_begin + j, n_tiles - 1), kKBuf + j * kTileBytes);
+        stage_mask(min(t_begin + j, n_tiles - 1));
+        if (j >= 2) stage_v(ln, min(t_begin + j - 2, n_tiles - 1), kVBuf + (j - 2) * kTileBytes);
+      }
     }
 #pragma unroll
     for (int p = 0; p < kTileBytes / (kThreads * 16); ++p)
@@ -365,8 +377,8 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
     // COPY (a compile-time tag): this wave issues tile copies. The 8-wave
     // workgroups run two copies of the loop, one for the copying waves and
     // one for the others, so that neither carries the other's branches.
-    auto step = [&](auto copy_tag, const int t, f32x16 (&S)[2], f32x16 (&Sn)[2], const bf16x8 (&Pp)[2][2],
-                    bf16x8 (&P)[2][2]) __attribute__((always_inline)) {
+    auto step = [&](auto copy_tag, const Lanes& ln, const int t, f32x16 (&S)[2], f32x16 (&Sn)[2],
+                    const bf16x8 (&Pp)[2][2], bf16x8 (&P)[2][2]) __attribute__((always_inline)) {
       constexpr bool COPY = decltype(copy_tag)::value;
       // K_{t+1} and V_{t-1} have landed once wait_prev returns; the barrier
       // then publishes them, and it also frees K buffer t % kNB (K_t, read by
@@ -391,9 +403,9 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
       if (MASK & kMaskFull) slow = true;
       // this iteration's copies: K_{t+kNB}, its mask and V_{t+kNB-2}
       if (COPY) {
-        stage_k(min(t + kNB, n_tiles - 1), kKBuf + kb_next * kTileBytes);
+        stage_k(ln, min(t + kNB, n_tiles - 1), kKBuf + kb_next * kTileBytes);
         stage_mask(min(t + kNB, n_tiles - 1));
-        stage_v(min(t + kNB - 2, n_tiles - 1), kVBuf + vb_next * kTileBytes);
+        stage_v(ln, min(t + kNB - 2, n_tiles - 1), kVBuf + vb_next * kTileBytes);
       }
       float cc = c;
       if (slow) {
@@ -537,13 +549,15 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
     f32x16 S2[2];
     bf16x8 P2[2][2];
     auto key_loop = [&](auto copy_tag) __attribute__((always_inline)) {
+      Lanes ln{};
+      if constexpr (decltype(copy_tag)::value) ln = make_lanes();
       int t = t_begin;
       for (; t + 1 < n_tiles; t += 2) {
-        step(copy_tag, t, S, S2, Pp, P2);
-        step(copy_tag, t + 1, S2, S, P2, Pp);
+        step(copy_tag, ln, t, S, S2, Pp, P2);
+        step(copy_tag, ln, t + 1, S2, S, P2, Pp);
       }
       if (t < n_tiles) {
-        step(copy_tag, t, S, S2, Pp, P2);
+        step(copy_tag, ln, t, S, S2, Pp, P2);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -584,7 +598,8 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
   u32x4 chunk[kDB][2];
   pack_out_rows<kDB>(O, inv, chunk);  // all lanes: cross-lane exchange
   if (qi < a.Sq) {
-    bf16* orow = og + (int64_t)qi * a.os[1];
+    // (the row address is formed here, so nothing of it is live in the key loop)
+    bf16* orow = (bf16*)a.o + (b * a.os[0] + head * a.os[2]) + (int64_t)qi * a.os[1];
 #pragma unroll
     for (int db = 0; db < kDB; ++db)
 #pragma unroll
@@ -678,7 +693,7 @@ const char* flash_split_kernel_name() {
 template <int MASK, int WAVES, int D>
 int launch_one(const FlashArgs& a, hipStream_t stream, const char** launched) {
   const int n_qt = (a.Sq + WAVES * 32 - 1) / (WAVES * 32);
-  if constexpr (!(MASK & kMaskFull)) {  // the per-(query, key) bias path is not split
+  if constexpr (!(MASK & (kMaskFull | kMaskBias))) {  // bias paths are not split
     if (a.split_items > 0) {
     const int n_items = n_qt * a.H * a.B;
     const int n_full = n_items - a.split_items;
@@ -697,11 +712,14 @@ int launch_one(const FlashArgs& a, hipStream_t stream, const char** launched) {
 }
 
 // The workgroup size (4 or 8 waves) comes from the launch plan in a.waves.
+// (the per-(query, key) bias path always runs 128-query workgroups)
 template <int MASK>
 int launch(const FlashArgs& a, hipStream_t stream, const char** launched) {
-  if (a.waves == 4)
+  if (a.waves == 4 || (MASK & kMaskFull))
     return a.D == 64 ? launch_one<MASK, 4, 64>(a, stream, launched) : launch_one<MASK, 4, 128>(a, stream, launched);
-  return a.D == 64 ? launch_one<MASK, 8, 64>(a, stream, launched) : launch_one<MASK, 8, 128>(a, stream, launched);
+  if constexpr (!(MASK & kMaskFull))
+    return a.D == 64 ? launch_one<MASK, 8, 64>(a, stream, launched) : launch_one<MASK, 8, 128>(a, stream, launched);
+  return (int)hipErrorInvalidValue;
 }
 
 }  // namespace

@@ -131,10 +131,16 @@ const FlashTileOverride& tile_override() {
   return o;
 }
 
-// Workgroup size for a flash call: the override, else the table's rule.
-int32_t flash_plan(int32_t B, int32_t Sq, int32_t Sk, int32_t H, int32_t* waves) {
+// Workgroup size for a flash call: the override, else the table's rule. A
+// per-(query, key) bias (the text encoders' short sequences) always runs
+// 128-query workgroups.
+int32_t flash_plan(int32_t B, int32_t Sq, int32_t Sk, int32_t H, bool full_bias, int32_t* waves) {
   const FlashTileOverride& o = tile_override();
   if (o.rc != VX_OK) return fail(o.rc, "%s", o.error.c_str());
+  if (full_bias) {
+    *waves = 4;
+    return VX_OK;
+  }
   if (o.block_q != 0) {
     *waves = o.block_q / 32;
     return VX_OK;
@@ -258,7 +264,7 @@ int32_t flash_check(const void* q, const void* k, const void* v, const void* out
     return fail(VX_ERR_UNSUPPORTED, "k/v sequence strides (%lld, %lld) above 2^24 elements are not supported",
                 (long long)ks[1], (long long)vs[1]);
   int32_t waves = 0;
-  if ((rc = flash_plan(B, Sq, Sk, H, &waves)) != VX_OK) return rc;
+  if ((rc = flash_plan(B, Sq, Sk, H, full_bias != nullptr, &waves)) != VX_OK) return rc;
   if (args != nullptr) {
     args->waves = waves;
     args->split_items = 0;
@@ -470,7 +476,7 @@ int32_t vx_flash_attn_split_plan(int32_t batch, int32_t seq_q, int32_t seq_k, in
   if (head_dim != 128 && head_dim != 64)
     return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 64 and 128)", head_dim);
   int32_t waves = 0;
-  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, &waves);
+  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, false, &waves);
   if (rc != VX_OK) return rc;
   const SplitPlan p = flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, waves, num_cus);
   if (split_items != nullptr) *split_items = p.items;
@@ -502,7 +508,10 @@ int32_t vx_flash_attn_ws_fwd(const void* q, const void* k, const void* v, void* 
   if (workspace != nullptr && !aligned16(workspace))
     return fail(VX_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   if ((rc = injected()) != VX_OK) return rc;
-  const SplitPlan p = flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, args.waves, vx::device_cu_count());
+  // (calls with a key bias are not split)
+  const SplitPlan p = key_bias != nullptr ? SplitPlan{}
+                                          : flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, args.waves,
+                                                             vx::device_cu_count());
   if (p.items > 0 && workspace != nullptr && workspace_bytes >= p.ws_bytes) {
     args.split_items = p.items;
     args.k_mid = p.k_mid;
@@ -523,7 +532,7 @@ int32_t vx_flash_attn_plan(int32_t batch, int32_t seq_q, int32_t seq_k, int32_t 
     return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 64 and 128)", head_dim);
   if (mask_kind < 0 || mask_kind > 7) return fail(VX_ERR_INVALID_ARGUMENT, "mask_kind must be in 0..7");
   int32_t waves = 0;
-  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, &waves);
+  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, (mask_kind & 4) != 0, &waves);
   if (rc != VX_OK) return rc;
   flash_kernel_label(mask_kind, head_dim, waves, kernel_name, name_len);
   return ok();
@@ -582,7 +591,9 @@ int32_t vx_flash_attn_noalloc_fwd(const void* q, const void* k, const void* v, v
                            num_heads, head_dim, q_strides, k_strides, v_strides, out_strides, scale, &args);
   if (rc != VX_OK) return rc;
   if ((rc = injected()) != VX_OK) return rc;
-  const SplitPlan p = flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, args.waves, vx::device_cu_count());
+  const SplitPlan p = key_bias != nullptr ? SplitPlan{}
+                                          : flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, args.waves,
+                                                             vx::device_cu_count());
   if (p.items > 0) {
     void* ws = nullptr;
     int64_t cap = 0;
