@@ -47,6 +47,16 @@ __device__ __forceinline__ int window_start(int i, int len, int k) {
   return min(max(i - k / 2, 0), len - k);
 }
 
+// Sum of a lane's 16 fp32 probabilities (pairwise).
+__device__ __forceinline__ float sum16(const float (&p)[16]) {
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = p[2 * i] + p[2 * i + 1];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) q[i] = q[2 * i] + q[2 * i + 1];
+  return (q[0] + q[1]) + (q[2] + q[3]);
+}
+
 // The block's q preparation on the resident Q fragments of one lane (query
 // `tok`, d = 16 * ds + 8 * hf + 0..7 in qr[ds]; lane l ^ 32 holds the other
 // half of the row), with the rounding points of the one-pass prologue kernel.
@@ -392,24 +402,28 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     head = blockIdx.y;
     brick = blockIdx.x;
   }
-  const int xb = brick % n_xb;
-  const int yb = (brick / n_xb) % n_yb;
-  const int t = brick / (n_xb * n_yb);
+  // The integer divisions below run on the vector unit; their (uniform)
+  // results go back to scalar registers, so the row walk stays scalar.
+  auto uni = [](int x) { return __builtin_amdgcn_readfirstlane(x); };
+  head = uni(head);
+  const int xb = uni(brick % n_xb);
+  const int yb = uni((brick / n_xb) % n_yb);
+  const int t = uni(brick / (n_xb * n_yb));
   const int b = blockIdx.z;
   const int T = a.T, Hs = a.Hs, W = a.W, kt = a.kt, kh = a.kh, kw = a.kw;
   const int y0 = yb * C::kBrickY, x0 = xb * C::kBrickX;
 
   // ---- the workgroup's key rows (box rows r = tr * NY + yr).
-  const int t_lo = window_start(t, T, kt);
-  const int Y_lo = window_start(y0, Hs, kh);
-  const int NY = window_start(min(y0 + C::kBrickY - 1, Hs - 1), Hs, kh) + kh - Y_lo;
-  const int X_lo = window_start(x0, W, kw);
+  const int t_lo = uni(window_start(t, T, kt));
+  const int Y_lo = uni(window_start(y0, Hs, kh));
+  const int NY = uni(window_start(min(y0 + C::kBrickY - 1, Hs - 1), Hs, kh) + kh - Y_lo);
+  const int X_lo = uni(window_start(x0, W, kw));
   const int nrows = kt * NY;
   const int n_steps = (nrows + C::kRows - 1) / C::kRows;
 
   // ---- this wave's queries: y rows y0..y0+kBrickY-1, x columns xq0..xq0+kQX-1.
   const int xq0 = x0 + C::kQX * wave;
-  const int ox = window_start(min(xq0, W - 1), W, kw) - X_lo;  // wave's first x slot, <= kBrickX - kQX
+  const int ox = uni(window_start(min(xq0, W - 1), W, kw) - X_lo);  // wave's first x slot, <= kBrickX - kQX
 
   // ---- this lane's query and its window.
   const int yq = y0 + col / C::kQX, xq = xq0 + col % C::kQX;
@@ -418,17 +432,19 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   const int yqc = min(yq, Hs - 1), xqc = min(xq, W - 1);
   const int sy = window_start(yqc, Hs, kh) - Y_lo;
   const int sx = window_start(xqc, W, kw) - X_lo - ox;  // in [0, SEG - kw]
-  // Per score register i (key (i/4)*8 + hf*4 + i%4 of the chunk): +inf if
-  // its x slot lies in this lane's window, -inf otherwise.
-  float xlim[16];
+  // Per score register i (key (i/4)*8 + hf*4 + i%4 of the chunk): 0 if its
+  // x slot lies in this lane's window, -inf otherwise. Every chunk's QK^T
+  // MFMAs start from it (the accumulator input of the first one), so the x
+  // window costs no instruction per score.
+  f32x16 xbias;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int p = (SEG == 16 ? ((i >> 2) & 1) * 8 : (i >> 2) * 8) + hf * 4 + (i & 3);
-    xlim[i] = (unsigned)(p - sx) < (unsigned)kw ? __builtin_inff() : -__builtin_inff();
+    xbias[i] = (unsigned)(p - sx) < (unsigned)kw ? 0.0f : -__builtin_inff();
   }
 
   const int64_t tok_stride = (int64_t)a.NH * D;
-  const int64_t head_off = (int64_t)b * T * Hs * W * tok_stride + (int64_t)head * D;
+  const int64_t head_off = (int64_t)uniform_u64((uint64_t)((int64_t)b * T * Hs * W * tok_stride + (int64_t)head * D));
   const bf16* qg = (const bf16*)a.q + head_off;
   const bf16* kg = (const bf16*)a.k + head_off;
   const bf16* vg = (const bf16*)a.v + head_off;
@@ -476,6 +492,9 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   };
   const int64_t row_step = (int64_t)W * tok_stride;             // next y
   const int64_t plane_jump = (int64_t)(Hs - NY) * W * tok_stride;  // last y of a plane -> first y of the next
+  // The cursor is wave-uniform; moving it through readfirstlane keeps its
+  // arithmetic on the scalar unit (left to itself the compiler walked it in
+  // 64-bit vector registers: ~60 VALU instructions per step).
   auto advance = [&](Cursor& c) {
     if (c.r + 1 < nrows) {
       ++c.r;
@@ -485,6 +504,9 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
         c.tok += plane_jump;
       }
     }
+    c.r = __builtin_amdgcn_readfirstlane(c.r);
+    c.yr = __builtin_amdgcn_readfirstlane(c.yr);
+    c.tok = (int64_t)uniform_u64((uint64_t)c.tok);
   };
   const Cursor first = {0, 0, ((int64_t)t_lo * Hs + Y_lo) * W * tok_stride};
   // Issues the copies of one step (rows c, c+1) and moves c on by kRows rows.
@@ -544,7 +566,6 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   for (int db = 0; db < kDB; ++db) O[db] = f32x16{};
   float m_run = kNegBig, l_run = 0.f;
   const float c2 = a.scale * kLog2e;
-  const bf16x2 one2 = {(bf16)1.0f, (bf16)1.0f};
 
   // ---- prologue: K of steps 0 and 1 in flight, V slot 1 zeroed (it stands
   // in for the V of step -1, paired with P = 0), S = QK^T of chunk 0.
@@ -558,7 +579,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   if (a.q_prep != 0) prep_q(qr, hf, token(t, yqc, xqc), a);
   wait_vmem<0>();
   __syncthreads();
-  f32x16 S = f32x16{};
+  f32x16 S = xbias;
 #pragma unroll
   for (int ds = 0; ds < C::kQK; ++ds) S = mfma32x32x16(kfrag(lds + C::kK, ds), qr[ds], S);
   bf16x8 Pp[2] = {bf16x8{}, bf16x8{}};
@@ -571,17 +592,16 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     // K slot s%2 (K of s, read last step) and V slot s%2 (V of s-2).
     wait_vmem<0>();
     __syncthreads();
-    // window mask of chunk s: keys outside this lane's y window (per row) or
-    // x window (per register) -> -inf
-    float rlim[2];
+    // y window of chunk s: whether each of its key rows lies in this lane's
+    // window (the x window is in the scores already, as -inf)
+    bool row_ok[2];
     {
       Cursor c = vcur;
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {
         if (SEG == 16 && h2 == 1) advance(c);
         const int r = s * C::kRows + (SEG == 16 ? h2 : 0);
-        const bool row_ok = r < nrows && (unsigned)(c.yr - sy) < (unsigned)kh;
-        rlim[h2] = row_ok ? __builtin_inff() : -__builtin_inff();
+        row_ok[h2] = r < nrows && (unsigned)(c.yr - sy) < (unsigned)kh;
       }
     }
     issue(kg, C::kK + (s & 1) * C::kSlot, kcur);
@@ -600,9 +620,11 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     auto frag = [&](int i) -> bf16x8 {
       return i < C::kPV ? vfrag(vb, i / kDB, i % kDB) : kfrag(kb, i - C::kPV);
     };
-    Sn = f32x16{};
-    float l_tile = 0.f;
-    const float mneg = -m_run;
+    Sn = xbias;
+    // exponent offset per key row: -m_run, or -inf for a row outside the y
+    // window (exp2 then gives 0)
+    const float mrow[2] = {row_ok[0] ? -m_run : -__builtin_inff(), row_ok[1] ? -m_run : -__builtin_inff()};
+    float l_tile;
     bf16x8 fr[C::kSlots];
     float pf[16];
     // wave priority 1 while in the slots, ahead of the other workgroup's
@@ -632,11 +654,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int e = 8 * g + i;
-          S[e] = __builtin_fminf(__builtin_fminf(S[e], xlim[e]), rlim[e >> 3]);
-          pf[e] = __builtin_fmaf(S[e], c2, mneg);
-        }
+        for (int i = 0; i < 8; ++i) pf[8 * g + i] = __builtin_fmaf(S[8 * g + i], c2, mrow[g]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < 8; ++i) pf[8 * g + i] = fast_exp2(pf[8 * g + i]);
@@ -645,8 +663,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
         for (int i = 0; i < 4; ++i) pk[4 * g + i] = bf16x2{(bf16)pf[8 * g + 2 * i], (bf16)pf[8 * g + 2 * i + 1]};
         __builtin_amdgcn_sched_barrier(0);
       }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[i], one2, l_tile, false);
+      l_tile = sum16(pf);
       __builtin_amdgcn_sched_barrier(0);
     } else {
 #pragma unroll
@@ -659,15 +676,12 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 #pragma unroll
         for (int u = 0; u < C::kScoresPerSlot; ++u) {
           const int e = i * C::kScoresPerSlot + u;
-          S[e] = __builtin_fminf(__builtin_fminf(S[e], xlim[e]), rlim[e >> 3]);
-          pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, mneg));
-          if (e & 1) {
-            pk[e >> 1] = bf16x2{(bf16)pf[e - 1], (bf16)pf[e]};
-            l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[e >> 1], one2, l_tile, false);
-          }
+          pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, mrow[e >> 3]));
+          if (e & 1) pk[e >> 1] = bf16x2{(bf16)pf[e - 1], (bf16)pf[e]};
         }
         __builtin_amdgcn_sched_barrier(0);
       }
+      l_tile = sum16(pf);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -680,24 +694,26 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     // always lands here) -> raise m_run to the chunk max, rescale O and l and
     // recompute the chunk's probabilities.
     if (__builtin_amdgcn_ballot_w64(l_tile > kSumLimit || is_nan_bits(l_tile)) != 0) {
-      float mx = S[0];
+      float mx = -__builtin_inff();
 #pragma unroll
-      for (int i = 1; i < 16; ++i) mx = __builtin_fmaxf(mx, S[i]);
+      for (int i = 0; i < 16; ++i) mx = __builtin_fmaxf(mx, row_ok[i >> 3] ? S[i] : -__builtin_inff());
       const float mn = __builtin_fmaxf(m_run, halves_max(mx) * c2);
       const float alpha = fast_exp2(m_run - mn);
       m_run = mn;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < kDB; ++db) O[db] *= alpha;
-      l_tile = 0.f;
+      const float mr[2] = {row_ok[0] ? -mn : -__builtin_inff(), row_ok[1] ? -mn : -__builtin_inff()};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, mr[e >> 3]));
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         bf16x8 pv;
 #pragma unroll
-        for (int r = 0; r < 8; ++r) pv[r] = (bf16)fast_exp2(__builtin_fmaf(S[8 * j + r], c2, -mn));
+        for (int r = 0; r < 8; ++r) pv[r] = (bf16)pf[8 * j + r];
         P[j] = pv;
-        l_tile = sum8(pv, l_tile);
       }
+      l_tile = sum16(pf);
     }
     l_run += l_tile;
   };
