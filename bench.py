@@ -215,12 +215,28 @@ def _traffic(kernel_name, workload):
     scaled by the same counters' reading for a plain copy of known size."""
     try:
         with open(TRAFFIC_FILE) as f:
-            rec = json.load(f).get("workloads", {}).get(workload, {})
+            stored = json.load(f)
     except (OSError, ValueError):
         return None
-    if rec.get("kernel") != kernel_name:
+    rec = stored.get("workloads", {}).get(workload, {})
+    # a figure measured on other kernel sources (any file under csrc/) is stale
+    if rec.get("kernel") != kernel_name or stored.get("csrc_sha256_16") != _csrc_hash():
         return None
     return rec.get("hbm_bytes_per_launch")
+
+
+def _csrc_hash():
+    """First 16 hex digits of the SHA-256 of the kernel sources (vidax_amd/csrc,
+    sorted by path), which the stored traffic figures were measured with."""
+    import glob
+    import hashlib
+    csrc = os.path.join(ROOT, "vidax_amd", "csrc")
+    paths = sorted(p for ext in ("*.hip", "*.hpp", "*.h", "*.cpp") for p in glob.glob(os.path.join(csrc, ext)))
+    h = hashlib.sha256()
+    for p in paths:
+        with open(p, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
 
 
 def _copy_calibration(mib, steps):

@@ -432,16 +432,25 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   const int yqc = min(yq, Hs - 1), xqc = min(xq, W - 1);
   const int sy = window_start(yqc, Hs, kh) - Y_lo;
   const int sx = window_start(xqc, W, kw) - X_lo - ox;  // in [0, SEG - kw]
-  // Per score register i (key (i/4)*8 + hf*4 + i%4 of the chunk): 0 if its
-  // x slot lies in this lane's window, -inf otherwise. Every chunk's QK^T
-  // MFMAs start from it (the accumulator input of the first one), so the x
-  // window costs no instruction per score.
+  // The x window of score register i (key (i/4)*8 + hf*4 + i%4 of the
+  // chunk). kAccMask: a 0 / -inf vector that every chunk's QK^T MFMAs start
+  // from (the first one's accumulator input), so the x window costs no
+  // instruction per score. Otherwise (the tall bricks at head dim 64, whose
+  // short steps need four waves per SIMD, i.e. at most 128 VGPRs, which the
+  // extra accumulator input does not leave) +inf / -inf limits applied with
+  // one v_min3 per score together with the row's y/t limit, and row sums of
+  // the bf16 probabilities.
+  constexpr bool kAccMask = !(TALL && D == 64);
   f32x16 xbias;
+  float xlim[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int p = (SEG == 16 ? ((i >> 2) & 1) * 8 : (i >> 2) * 8) + hf * 4 + (i & 3);
-    xbias[i] = (unsigned)(p - sx) < (unsigned)kw ? 0.0f : -__builtin_inff();
+    const bool in = (unsigned)(p - sx) < (unsigned)kw;
+    xbias[i] = in ? 0.0f : -__builtin_inff();
+    xlim[i] = in ? __builtin_inff() : -__builtin_inff();
   }
+  const f32x16 s_init = kAccMask ? xbias : f32x16{};
 
   const int64_t tok_stride = (int64_t)a.NH * D;
   const int64_t head_off = (int64_t)uniform_u64((uint64_t)((int64_t)b * T * Hs * W * tok_stride + (int64_t)head * D));
@@ -579,7 +588,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   if (a.q_prep != 0) prep_q(qr, hf, token(t, yqc, xqc), a);
   wait_vmem<0>();
   __syncthreads();
-  f32x16 S = xbias;
+  f32x16 S = s_init;
 #pragma unroll
   for (int ds = 0; ds < C::kQK; ++ds) S = mfma32x32x16(kfrag(lds + C::kK, ds), qr[ds], S);
   bf16x8 Pp[2] = {bf16x8{}, bf16x8{}};
@@ -620,11 +629,14 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     auto frag = [&](int i) -> bf16x8 {
       return i < C::kPV ? vfrag(vb, i / kDB, i % kDB) : kfrag(kb, i - C::kPV);
     };
-    Sn = xbias;
+    Sn = s_init;
     // exponent offset per key row: -m_run, or -inf for a row outside the y
     // window (exp2 then gives 0)
     const float mrow[2] = {row_ok[0] ? -m_run : -__builtin_inff(), row_ok[1] ? -m_run : -__builtin_inff()};
-    float l_tile;
+    const float rlim[2] = {row_ok[0] ? __builtin_inff() : -__builtin_inff(),
+                           row_ok[1] ? __builtin_inff() : -__builtin_inff()};
+    const bf16x2 one2 = {(bf16)1.0f, (bf16)1.0f};
+    float l_tile = 0.f;
     bf16x8 fr[C::kSlots];
     float pf[16];
     // wave priority 1 while in the slots, ahead of the other workgroup's
@@ -654,7 +666,11 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) pf[8 * g + i] = __builtin_fmaf(S[8 * g + i], c2, mrow[g]);
+        for (int i = 0; i < 8; ++i) {
+          // (the tall D = 64 block: kAccMask is false)
+          S[8 * g + i] = __builtin_fminf(__builtin_fminf(S[8 * g + i], xlim[8 * g + i]), rlim[g]);
+          pf[8 * g + i] = __builtin_fmaf(S[8 * g + i], c2, -m_run);
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < 8; ++i) pf[8 * g + i] = fast_exp2(pf[8 * g + i]);
@@ -663,7 +679,11 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
         for (int i = 0; i < 4; ++i) pk[4 * g + i] = bf16x2{(bf16)pf[8 * g + 2 * i], (bf16)pf[8 * g + 2 * i + 1]};
         __builtin_amdgcn_sched_barrier(0);
       }
-      l_tile = sum16(pf);
+      // row sums of the bf16 probabilities (dot2 with 1, 1): fp32 sums of
+      // the unrounded ones keep pf live past the packing, 5 spills at 128 VGPRs
+      l_tile = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[i], one2, l_tile, false);
       __builtin_amdgcn_sched_barrier(0);
     } else {
 #pragma unroll
@@ -676,12 +696,20 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 #pragma unroll
         for (int u = 0; u < C::kScoresPerSlot; ++u) {
           const int e = i * C::kScoresPerSlot + u;
-          pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, mrow[e >> 3]));
-          if (e & 1) pk[e >> 1] = bf16x2{(bf16)pf[e - 1], (bf16)pf[e]};
+          if constexpr (kAccMask) {
+            pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, mrow[e >> 3]));
+          } else {
+            S[e] = __builtin_fminf(__builtin_fminf(S[e], xlim[e]), rlim[e >> 3]);
+            pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, -m_run));
+          }
+          if (e & 1) {
+            pk[e >> 1] = bf16x2{(bf16)pf[e - 1], (bf16)pf[e]};
+            if constexpr (!kAccMask) l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[e >> 1], one2, l_tile, false);
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      l_tile = sum16(pf);
+      if constexpr (kAccMask) l_tile = sum16(pf);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -694,26 +722,40 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     // always lands here) -> raise m_run to the chunk max, rescale O and l and
     // recompute the chunk's probabilities.
     if (__builtin_amdgcn_ballot_w64(l_tile > kSumLimit || is_nan_bits(l_tile)) != 0) {
+      // (with kAccMask the scores carry the x window only; without it S is
+      // fully masked already)
       float mx = -__builtin_inff();
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = __builtin_fmaxf(mx, row_ok[i >> 3] ? S[i] : -__builtin_inff());
+      for (int i = 0; i < 16; ++i) mx = __builtin_fmaxf(mx, !kAccMask || row_ok[i >> 3] ? S[i] : -__builtin_inff());
       const float mn = __builtin_fmaxf(m_run, halves_max(mx) * c2);
       const float alpha = fast_exp2(m_run - mn);
       m_run = mn;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < kDB; ++db) O[db] *= alpha;
-      const float mr[2] = {row_ok[0] ? -mn : -__builtin_inff(), row_ok[1] ? -mn : -__builtin_inff()};
+      if constexpr (kAccMask) {
+        const float mr[2] = {row_ok[0] ? -mn : -__builtin_inff(), row_ok[1] ? -mn : -__builtin_inff()};
 #pragma unroll
-      for (int e = 0; e < 16; ++e) pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, mr[e >> 3]));
+        for (int e = 0; e < 16; ++e) pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, mr[e >> 3]));
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        bf16x8 pv;
+        for (int j = 0; j < 2; ++j) {
+          bf16x8 pv;
 #pragma unroll
-        for (int r = 0; r < 8; ++r) pv[r] = (bf16)pf[8 * j + r];
-        P[j] = pv;
+          for (int r = 0; r < 8; ++r) pv[r] = (bf16)pf[8 * j + r];
+          P[j] = pv;
+        }
+        l_tile = sum16(pf);
+      } else {
+        l_tile = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          bf16x8 pv;
+#pragma unroll
+          for (int r = 0; r < 8; ++r) pv[r] = (bf16)fast_exp2(__builtin_fmaf(S[8 * j + r], c2, -mn));
+          P[j] = pv;
+          l_tile = sum8(pv, l_tile);
+        }
       }
-      l_tile = sum16(pf);
     }
     l_run += l_tile;
   };
@@ -758,8 +800,11 @@ void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   na3d_pipe_body<SEG, D, false>(a, n_yb, n_xb);
 }
 
+// Head dim 64: four waves per SIMD (at most 128 VGPRs; the workgroup's 32 KiB
+// of LDS allows four per CU), so that more workgroups cover each other's
+// per-step waits: 2.56 -> 2.31 ms at the (11, 11, 11) window on 33x88x160.
 template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 2, D == 64 ? 4 : 2)))
 void na3d_tall_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   na3d_pipe_body<16, D, true>(a, n_yb, n_xb);
 }
