@@ -284,7 +284,11 @@ def test_na3d_kernel_name_follows_the_launch_rule():
     from vidax_amd.natten import na3d_kernel_name
     assert na3d_kernel_name(80, 7) == "na3d_pipe_kernel<16, 128>"
     assert na3d_kernel_name(80, 9, 64) == "na3d_pipe_kernel<16, 64>"
-    assert na3d_kernel_name(80, 11, 64) == "na3d_tall_kernel<64>"
+    assert na3d_kernel_name(80, 11, 64) == "na3d_tall_kernel<64>"        # 80 = 5 x 16, 96 in 32-wide bricks
+    assert na3d_kernel_name(160, 11, 64) == "na3d_tall_wide_kernel<64>"  # 160 = 5 x 32
+    assert na3d_kernel_name(104, 11, 64) == "na3d_tall_kernel<64>"       # 112 vs 128 columns
+    assert na3d_kernel_name(24, 13, 64) == "na3d_tall_wide_kernel<64>"   # 32 columns either way
+    assert na3d_kernel_name(160, 11) == "na3d_tall_kernel<128>"          # head dim 128: narrow bricks
     assert na3d_kernel_name(80, 13) == "na3d_tall_kernel<128>"
     assert na3d_kernel_name(12, 40) == "na3d_tall_kernel<128>"        # clamped to the grid width
     assert na3d_kernel_name(80, 14) == "na3d_pipe_kernel<32, 128>"

@@ -62,6 +62,9 @@ def _expected_kernel(W, kw, D):
     if k <= 9:
         return f"na3d_pipe_kernel<16, {D}>"
     if k <= 13:
+        # head dim 64: 32-wide bricks unless they leave more ragged columns
+        if D == 64 and -(-W // 32) * 32 == -(-W // 16) * 16:
+            return "na3d_tall_wide_kernel<64>"
         return f"na3d_tall_kernel<{D}>"
     if k <= 25:
         return f"na3d_pipe_kernel<32, {D}>"
@@ -94,6 +97,8 @@ NA_D64_CASES = [
     ((1, 3, 9, 40, 4), (3, 3, 25), 54),       # widest x window for head dim 64
     ((1, 13, 21, 35, 2), (11, 11, 11), 55),   # stage-5 window, ragged tall bricks
     ((1, 3, 12, 40, 2), (3, 9, 9), 56),       # empty waves at the ragged x edge
+    ((1, 5, 19, 64, 2), (5, 11, 11), 57),     # 32-wide tall bricks, two along x, ragged y
+    ((2, 4, 10, 56, 1), (3, 13, 12), 58),     # 32-wide tall bricks, even window, two empty waves at x
 ]
 
 

@@ -12,7 +12,8 @@
 //   with the masking and lazy-rescale softmax of the current one).
 // - na3d_tall_kernel<D> (9 < kw' <= 13): the same body on 1 x 8 x 16 bricks
 //   with waves of 8 y x 4 x queries, so that a wave's x window still fits a
-//   16-key segment.
+//   16-key segment; na3d_tall_wide_kernel<64> runs 1 x 8 x 32 bricks of 8
+//   such waves at head dim 64.
 // - na3d_wave_kernel (25 < kw' <= 57, D = 128): each wave owns a
 //   1 x 4 x 8 brick on its own and walks its (kt', ny, nx) key box in chunks
 //   of 32 keys, laid out as (t', y') rows of SEG = round_up(nx, 16)
@@ -343,17 +344,22 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
 // scored with 18 rows x 16 keys per plane instead of the 14 x 32 of the
 // 32-key segments.
 
-template <int SEG, int D, bool TALL = false>
+// WIDE: tall bricks 32 x columns wide with 8 waves (each still 8 y x 4 x):
+// the 42-key x union of a row is staged in 48 slots for 32 queries (26 in
+// 32 for 16 with the narrow brick), one workgroup barrier per step for
+// twice the queries.
+template <int SEG, int D, bool TALL = false, bool WIDE = false>
 struct PipeCfg {
   static_assert(!TALL || SEG == 16, "the tall geometry reads 16-key segments");
-  static constexpr int kWaves = 4;
+  static_assert(!WIDE || TALL, "wide bricks are tall bricks");
+  static constexpr int kWaves = WIDE ? 8 : 4;
   static constexpr int kThreads = kWaves * 64;
-  static constexpr int kBrickY = TALL ? 8 : 4, kBrickX = TALL ? 16 : 32;
+  static constexpr int kBrickY = TALL ? 8 : 4, kBrickX = TALL ? (WIDE ? 32 : 16) : 32;
   static constexpr int kQX = kBrickX / kWaves;           // x columns per wave (32 / kQX y rows)
   static constexpr int kRB = D * 2;                      // bytes of one key
   static constexpr int kRows = SEG == 16 ? 2 : 1;        // key rows per step
   // key slots per LDS row (>= kBrickX - kQX + SEG, a multiple of 8)
-  static constexpr int kNS = TALL ? 32 : (SEG == 16 ? 40 : 64);
+  static constexpr int kNS = TALL ? (WIDE ? 48 : 32) : (SEG == 16 ? 40 : 64);
   // An LDS key row is D/64 half-planes of kNS slots x 128 bytes (d 0-63,
   // then d 64-127); one 1 KiB DMA copy fills 8 slots of one half-plane.
   static constexpr int kHalfL = kNS * 128;               // one half-plane of a row
@@ -363,8 +369,8 @@ struct PipeCfg {
   static constexpr int kK = 0, kV = 2 * kSlot;           // K slots 0,1 then V slots 0,1
   static constexpr int kSmem = 4 * kSlot;
   static constexpr int kCopies = kRows * kRowL / 1024;   // DMA copies per tensor per step
-  // copies past kCopies repeat the last one (same bytes, same place), so every
-  // wave issues the same number of copies
+  // the copies of a step spread over the waves (those past kCopies are skipped;
+  // every wait for them is a wait for all of a wave's copies)
   static constexpr int kCopiesPerWave = (kCopies + kWaves - 1) / kWaves;
   static constexpr int kQK = D / 16;                     // MFMAs of QK^T per chunk
   static constexpr int kPV = 2 * (D / 32);               // MFMAs of PV per chunk
@@ -373,9 +379,9 @@ struct PipeCfg {
   static_assert(kNS % kKeysPerCopy == 0 && kHalfL % 256 == 0, "whole copies per row, bank-aligned planes");
 };
 
-template <int SEG, int D, bool TALL>
+template <int SEG, int D, bool TALL, bool WIDE = false>
 __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int n_xb) {
-  using C = PipeCfg<SEG, D, TALL>;
+  using C = PipeCfg<SEG, D, TALL, WIDE>;
   static_assert(C::kBrickX - C::kQX + SEG <= C::kNS, "a wave's segment stays inside the LDS row");
   __shared__ __attribute__((aligned(16))) unsigned char smem[C::kSmem];
   VX_LDS unsigned char* const lds = (VX_LDS unsigned char*)smem;
@@ -526,7 +532,8 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     if (C::kRows == 2) advance(c);
 #pragma unroll
     for (int p = 0; p < C::kCopiesPerWave; ++p)
-      lds_dma16_buf(raw_rsrc(base + (dma_row[p] ? rt1 : rt0)), dma_voff[p], lds_base + slot_off + dma_dst[p]);
+      if (C::kCopies % C::kWaves == 0 || wave + C::kWaves * p < C::kCopies)
+        lds_dma16_buf(raw_rsrc(base + (dma_row[p] ? rt1 : rt0)), dma_voff[p], lds_base + slot_off + dma_dst[p]);
   };
 
   // ---- per-lane LDS offsets (half-plane 0; d 64-127 add kHalfL). K
@@ -809,6 +816,15 @@ void na3d_tall_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   na3d_pipe_body<16, D, true>(a, n_yb, n_xb);
 }
 
+// Head dim 64, grids whose width rounds up to the same multiple of 16 and 32
+// (no more ragged columns than the narrow bricks): 1 x 8 x 32 bricks of 8
+// waves, two workgroups of 48 KiB per CU. 33x88x160: 2.31 -> 2.09 ms.
+template <int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void na3d_tall_wide_kernel(const Na3dArgs a, int n_yb, int n_xb) {
+  na3d_pipe_body<16, D, true, true>(a, n_yb, n_xb);
+}
+
 }  // namespace
 
 int launch_na3d_fwd(const Na3dArgs& a, void* stream, const char** launched) {
@@ -826,6 +842,15 @@ int launch_na3d_fwd(const Na3dArgs& a, void* stream, const char** launched) {
         hipLaunchKernelGGL((na3d_tall_kernel<64>), grid, dim3(256), 0, st, a, n_yb, n_xb);
         *launched = "na3d_tall_kernel<64>";
       }
+      return (int)hipGetLastError();
+    }
+    case kNaTallWide: {
+      if (a.D != 64) return (int)hipErrorNotSupported;
+      const int n_yb = (a.Hs + 7) / 8;
+      const int n_xb = (a.W + 31) / 32;
+      dim3 grid((unsigned)a.T * n_yb * n_xb, a.NH, a.B);
+      hipLaunchKernelGGL((na3d_tall_wide_kernel<64>), grid, dim3(512), 0, st, a, n_yb, n_xb);
+      *launched = "na3d_tall_wide_kernel<64>";
       return (int)hipGetLastError();
     }
     case kNaPipe16:

@@ -188,12 +188,13 @@ SplitPlan flash_split_plan(int32_t B, int32_t Sq, int32_t Sk, int32_t H, int32_t
   return p;
 }
 
-// ---- neighbourhood-attention launch plan, by the clamped x window.
-int32_t na3d_variant(int32_t kw_clamped, int32_t D) {
+// ---- neighbourhood-attention launch plan, by the clamped x window (and for
+// head dim 64 with the tall bricks, the grid width: the 32-wide bricks when
+// they leave no more ragged columns than the 16-wide ones).
+int32_t na3d_variant(int32_t kw_clamped, int32_t D, int32_t W) {
   if (kw_clamped <= 9) return vx::kNaPipe16;
-  if (kw_clamped <= 13) return vx::kNaTall;
+  if (kw_clamped <= 13) return D == 64 && (W + 31) / 32 * 32 == (W + 15) / 16 * 16 ? vx::kNaTallWide : vx::kNaTall;
   if (kw_clamped <= 25) return vx::kNaPipe32;
-  (void)D;
   return vx::kNaWave;
 }
 
@@ -201,6 +202,7 @@ const char* na3d_kernel_label(int32_t variant, int32_t D) {
   switch (variant) {
     case vx::kNaPipe16: return D == 64 ? "na3d_pipe_kernel<16, 64>" : "na3d_pipe_kernel<16, 128>";
     case vx::kNaTall: return D == 64 ? "na3d_tall_kernel<64>" : "na3d_tall_kernel<128>";
+    case vx::kNaTallWide: return "na3d_tall_wide_kernel<64>";
     case vx::kNaPipe32: return D == 64 ? "na3d_pipe_kernel<32, 64>" : "na3d_pipe_kernel<32, 128>";
     default: return "na3d_wave_kernel";
   }
@@ -342,7 +344,7 @@ int32_t na3d_check(const void* q, const void* k, const void* v, const void* out,
     args->kh = kh < Hs ? kh : Hs;
     args->kw = kw < W ? kw : W;
     args->scale = scale;
-    args->variant = na3d_variant(args->kw, D);
+    args->variant = na3d_variant(args->kw, D, W);
     args->q_prep = 0;
     args->q_weight = nullptr;
     args->q_cos = args->q_sin = nullptr;
@@ -548,7 +550,7 @@ int32_t vx_na3d_plan(int32_t t, int32_t h, int32_t w, int32_t head_dim, int32_t 
   if (rc != VX_OK) return rc;
   const int32_t kw = kernel_w < w ? kernel_w : w;
   if (kernel_name != nullptr && name_len > 0)
-    snprintf(kernel_name, (size_t)name_len, "%s", na3d_kernel_label(na3d_variant(kw, head_dim), head_dim));
+    snprintf(kernel_name, (size_t)name_len, "%s", na3d_kernel_label(na3d_variant(kw, head_dim, w), head_dim));
   return ok();
 }
 

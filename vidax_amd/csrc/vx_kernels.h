@@ -71,6 +71,7 @@ enum Na3dVariant : int32_t {
   kNaTall = 1,    // 9 < kw' <= 13: the same body on 1 x 8 x 16 bricks
   kNaPipe32 = 2,  // 13 < kw' <= 25: 32-key x segments
   kNaWave = 3,    // 25 < kw' <= 57, head dim 128: per-wave bricks
+  kNaTallWide = 4,  // head dim 64, 9 < kw' <= 13, round_up(W, 32) == round_up(W, 16): 1 x 8 x 32 bricks
 };
 
 struct PrologueArgs {
