@@ -26,7 +26,7 @@ extern "C" {
 #define VX_ERR_UNSUPPORTED 2      /* a valid request this build has no kernel for   */
 #define VX_ERR_LAUNCH 3           /* the HIP runtime refused the launch             */
 
-/* Version of this ABI (major * 10000 + minor * 100 + patch): 1.5.0. */
+/* Version of this ABI (major * 10000 + minor * 100 + patch): 1.6.0. */
 int32_t vx_abi_version(void);
 
 /* Message describing the most recent failure on the calling thread ("" if none). */
@@ -196,10 +196,10 @@ int32_t vx_flash_attn_check(const void* q, const void* k, const void* v, const v
  * diffusion_vae.py:152-164 (_window_start).
  *
  * Tensors are contiguous (B, T, Hs, W, NH, D) bf16, 16-byte aligned.
- * Supported: head_dim 128 with 1 <= kt, kh, kw and min(kw, w) <= 57, or
- * head_dim 64 (the LTX-2.5 diffusion VAE's, src/vidax/models/ltx2_5/configs.py:
- * 194-203) with min(kw, w) <= 25; all sizes >= 1; batch, num_heads <= 65535;
- * w * num_heads * head_dim < 2^30 (one row of tokens).
+ * Supported: head_dim 128 or 64 (the LTX-2.5 diffusion VAE's,
+ * src/vidax/models/ltx2_5/configs.py:194-203), any window (kt, kh, kw >= 1;
+ * windows wider than the grid are clamped to it); all sizes >= 1; batch,
+ * num_heads <= 65535; w * num_heads * head_dim < 2^30 (one row of tokens).
  */
 int32_t vx_na3d_fwd(const void* q, const void* k, const void* v, void* out, int32_t batch,
                     int32_t t, int32_t h, int32_t w, int32_t num_heads, int32_t head_dim,

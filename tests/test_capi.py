@@ -32,7 +32,7 @@ def test_header_symbols_are_exported():
 
 
 def test_abi_version():
-    assert _lib.lib().vx_abi_version() == 10500
+    assert _lib.lib().vx_abi_version() == 10600
 
 
 def _flash_check(**kw):
@@ -92,11 +92,13 @@ def test_na3d_check():
     assert _na_check() == _lib.VX_OK
     assert _na_check(kt=100, kh=100, kw=100) == _lib.VX_OK          # clamped to the grid
     assert _na_check(W=200, kw=57) == _lib.VX_OK
-    assert _na_check(W=200, kw=58) == _lib.VX_ERR_UNSUPPORTED
+    assert _na_check(W=200, kw=58) == _lib.VX_OK                     # any window (per-wave kernel)
+    assert _na_check(W=300, kh=40, kw=199) == _lib.VX_OK
     assert _na_check(kt=0) == _lib.VX_ERR_INVALID_ARGUMENT
     assert _na_check(D=64) == _lib.VX_OK                             # LTX-2.5 VAE head dim
     assert _na_check(D=64, W=200, kw=25) == _lib.VX_OK
-    assert _na_check(D=64, W=200, kw=27) == _lib.VX_ERR_UNSUPPORTED
+    assert _na_check(D=64, W=200, kw=27) == _lib.VX_OK
+    assert _na_check(D=64, W=200, kw=99) == _lib.VX_OK
     assert _na_check(D=96) == _lib.VX_ERR_UNSUPPORTED
     assert _na_check(T=0) == _lib.VX_ERR_INVALID_ARGUMENT
     assert _na_check(k=A + 1) == _lib.VX_ERR_INVALID_ARGUMENT
@@ -293,7 +295,9 @@ def test_na3d_kernel_name_follows_the_launch_rule():
     assert na3d_kernel_name(12, 40) == "na3d_tall_kernel<128>"        # clamped to the grid width
     assert na3d_kernel_name(80, 14) == "na3d_pipe_kernel<32, 128>"
     assert na3d_kernel_name(80, 25, 64) == "na3d_pipe_kernel<32, 64>"
-    assert na3d_kernel_name(80, 27) == "na3d_wave_kernel"
+    assert na3d_kernel_name(80, 27) == "na3d_wave_kernel<128>"
+    assert na3d_kernel_name(80, 27, 64) == "na3d_wave_kernel<64>"
+    assert na3d_kernel_name(200, 99) == "na3d_wave_kernel<128>"
 
 
 def test_small_scale_without_key_bias_is_accepted():
@@ -426,7 +430,6 @@ def test_na3d_qprep_check():
         (dict(stride=62), _lib.VX_ERR_INVALID_ARGUMENT, "rope_stride"),
         (dict(stride=60), _lib.VX_ERR_INVALID_ARGUMENT, "rope_stride"),
         (dict(q=None), _lib.VX_ERR_INVALID_ARGUMENT, "non-NULL"),
-        (dict(kw=60), _lib.VX_ERR_UNSUPPORTED, "57"),
     ]:
         assert _qprep_check(**kw) == code, kw
         assert frag in _lib.last_error(), (kw, _lib.last_error())

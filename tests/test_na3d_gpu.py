@@ -43,7 +43,7 @@ NA_CASES = [
     ((1, 3, 9, 11, 1), (2, 4, 6), 34),     # even windows
     ((1, 2, 3, 4, 2), (5, 9, 9), 35),      # every window clamped: full attention
     ((1, 3, 4, 30, 1), (1, 1, 25), 36),    # wide x window (two 16-key segments)
-    ((1, 2, 4, 70, 1), (1, 3, 57), 37),    # widest supported x window (per-wave kernel)
+    ((1, 2, 4, 70, 1), (1, 3, 57), 37),    # per-wave kernel, x box of 64 slots
     ((1, 3, 10, 40, 2), (3, 11, 11), 41),  # 32-slot x windows (LTX-2.5 stage-5 shape family)
     ((1, 4, 17, 33, 1), (3, 5, 13), 42),
     ((2, 5, 9, 65, 2), (5, 3, 9), 43),     # ragged workgroup bricks along y and x
@@ -68,7 +68,7 @@ def _expected_kernel(W, kw, D):
         return f"na3d_tall_kernel<{D}>"
     if k <= 25:
         return f"na3d_pipe_kernel<32, {D}>"
-    return "na3d_wave_kernel"
+    return f"na3d_wave_kernel<{D}>"
 
 
 def _run(gpu, shape, ks, seed, D):
@@ -124,6 +124,25 @@ NA_NH8_CASES = [
 @pytest.mark.parametrize("shape,ks,seed,D", NA_NH8_CASES)
 def test_na3d_head_remap(gpu, shape, ks, seed, D):
     _say(f"na3d NH%8==0 shape={shape} kernel={ks} seed={seed} D={D}")
+    _run(gpu, shape, ks, seed, D)
+
+
+# Windows wider than 25 (any size, both head dims) run on the per-wave kernel,
+# whose x box is round_up(kw' + 7, 16) slots: beyond 64 slots, ragged y/x
+# bricks, the widest windows clamped to the grid.
+NA_WIDE_CASES = [
+    # (B, T, H, W, NH), kernel, seed, D
+    ((1, 2, 5, 90, 1), (1, 3, 75), 70, 128),     # 96-slot x box
+    ((1, 3, 6, 40, 2), (3, 3, 29), 71, 64),      # head dim 64 above 25
+    ((1, 2, 5, 100, 1), (1, 5, 85), 72, 64),     # head dim 64, 96-slot x box
+    ((2, 2, 9, 130, 1), (2, 3, 121), 73, 128),   # 128-slot x box, ragged y bricks, two batch items
+    ((1, 2, 4, 64, 8), (2, 3, 60), 74, 64),      # NH = 8
+]
+
+
+@pytest.mark.parametrize("shape,ks,seed,D", NA_WIDE_CASES)
+def test_na3d_wide_windows(gpu, shape, ks, seed, D):
+    _say(f"na3d wide window shape={shape} kernel={ks} seed={seed} D={D}")
     _run(gpu, shape, ks, seed, D)
 
 

@@ -30,10 +30,7 @@
 namespace vx {
 namespace {
 
-constexpr int kD = 128;
-constexpr int kRowBytes = kD * 2;
-constexpr int kChunk = 32;                       // keys per chunk
-constexpr int kChunkBytes = kChunk * kRowBytes;  // 8 KiB
+constexpr int kChunk = 32;  // keys per chunk of the per-wave kernel
 constexpr int kBrickY = 4;
 constexpr int kBrickX = 8;
 constexpr int kWaves = 4;
@@ -118,9 +115,16 @@ __device__ __forceinline__ void prep_q(bf16x8 (&qr)[NDS], int hf, int64_t tok, c
   }
 }
 
+template <int D>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
 void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[kWaves * 2 * kChunkBytes];
+  constexpr int kRB = D * 2;              // bytes of one key
+  constexpr int kCB = kChunk * kRB;       // one chunk of V in LDS
+  constexpr int kNDS = D / 16, kNDB = D / 32;
+  constexpr int kCPR = D / 8;             // 16-byte columns of a key row
+  constexpr int kRPP = 64 / kCPR;         // V rows a wave stages per pass
+  constexpr int kVPass = kChunk / kRPP;   // passes per chunk
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kWaves * 2 * kCB];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int hf = lane >> 5;
@@ -139,13 +143,13 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
   const int T = a.T, Hs = a.Hs, W = a.W, kt = a.kt, kh = a.kh, kw = a.kw;
   const int y0 = yb * kBrickY, x0 = xb * kBrickX;
 
-  // ---- the brick's key box.
+  // ---- the brick's key box: kt' x ny rows of seg = round_up(nx, 16) x slots.
   const int t_lo = window_start(t, T, kt);
   const int y_lo = window_start(y0, Hs, kh);
   const int ny = window_start(min(y0 + kBrickY - 1, Hs - 1), Hs, kh) + kh - y_lo;
   const int x_lo = window_start(x0, W, kw);
   const int nx = window_start(min(x0 + kBrickX - 1, W - 1), W, kw) + kw - x_lo;
-  const int seg = (nx + 15) & ~15;  // <= 64 (checked on the host)
+  const int seg = (nx + 15) & ~15;
   const int nrows = kt * ny;
   const int n_chunks = (nrows * seg + kChunk - 1) / kChunk;
 
@@ -155,11 +159,10 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
   const int yqc = min(yq, Hs - 1), xqc = min(xq, W - 1);
   const int sy = window_start(yqc, Hs, kh) - y_lo;
   const int sx = window_start(xqc, W, kw) - x_lo;
-  const uint64_t xmask = (kw >= 64 ? ~0ull : ((1ull << kw) - 1)) << sx;
 
-  const int64_t tok_stride = (int64_t)a.NH * kD;  // elements between tokens
+  const int64_t tok_stride = (int64_t)a.NH * D;  // elements between tokens
   const int64_t plane = (int64_t)T * Hs * W;
-  const int64_t head_off = (int64_t)b * plane * tok_stride + (int64_t)head * kD;
+  const int64_t head_off = (int64_t)b * plane * tok_stride + (int64_t)head * D;
   const bf16* qg = (const bf16*)a.q + head_off;
   const bf16* kg = (const bf16*)a.k + head_off;
   const bf16* vg = (const bf16*)a.v + head_off;
@@ -167,15 +170,15 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
   auto token = [&](int tt, int yy, int xx) -> int64_t { return ((int64_t)tt * Hs + yy) * W + xx; };
 
   // ---- Q fragments (B operand), resident.
-  bf16x8 qr[8];
+  bf16x8 qr[kNDS];
   {
     const bf16* p = qg + token(t, yqc, xqc) * tok_stride + hf * 8;
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
+    for (int ds = 0; ds < kNDS; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
   }
   if (a.q_prep != 0) prep_q(qr, hf, token(t, yqc, xqc), a);
 
-  // Token index of key j of a 16-key half chunk starting at box key kb2.
+  // Box row and first x slot of the 16-key half chunk starting at box key kb2.
   auto half_row = [&](int kb2, int& trow, int& j0) {
     int row = kb2 / seg;
     j0 = kb2 - row * seg;
@@ -188,36 +191,38 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
   };
 
   // K fragment of chunk c for this lane: key row col of the chunk.
-  bf16x8 kf[8], kfn[8];
+  bf16x8 kf[kNDS], kfn[kNDS];
   auto load_k = [&](int c, bf16x8* dst) {
     int row, j0;
     half_row(c * kChunk + (col & 16), row, j0);
     const bf16* p = kg + row_token(row, j0 + (col & 15)) * tok_stride + hf * 8;
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) dst[ds] = *(const bf16x8*)(p + ds * 16);
+    for (int ds = 0; ds < kNDS; ++ds) dst[ds] = *(const bf16x8*)(p + ds * 16);
   };
-  // V rows of chunk c: lane covers rows 4p + lane/16 (p = 0..7), 16-byte column lane%16.
-  u32x4 vst[8];
+  // V rows of chunk c: pass p covers rows kRPP * p + lane / kCPR, 16-byte
+  // column lane % kCPR (rows 0-15 from one box row, 16-31 from the next
+  // half chunk's).
+  u32x4 vst[kVPass];
   auto load_v = [&](int c) {
+    int rowa, j0a, rowb, j0b;
+    half_row(c * kChunk, rowa, j0a);
+    half_row(c * kChunk + 16, rowb, j0b);
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-      int row, j0;
-      half_row(c * kChunk + 16 * h2, row, j0);
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int r = 4 * p + (lane >> 4);  // row within the half chunk
-        const bf16* src = vg + row_token(row, j0 + r) * tok_stride + (lane & 15) * 8;
-        vst[4 * h2 + p] = *(const u32x4*)src;
-      }
+    for (int p = 0; p < kVPass; ++p) {
+      const int r = kRPP * p + lane / kCPR;
+      const bool second = r >= 16;
+      const bf16* src = vg + row_token(second ? rowb : rowa, (second ? j0b : j0a) + (r & 15)) * tok_stride +
+                        (lane % kCPR) * 8;
+      vst[p] = *(const u32x4*)src;
     }
   };
-  unsigned char* const vbuf0 = smem + wave * 2 * kChunkBytes;
-  unsigned char* const vbuf1 = vbuf0 + kChunkBytes;
+  unsigned char* const vbuf0 = smem + wave * 2 * kCB;
+  unsigned char* const vbuf1 = vbuf0 + kCB;
   auto store_v = [&](unsigned char* buf) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = 16 * (i >> 2) + 4 * (i & 3) + (lane >> 4);
-      *(u32x4*)(buf + r * kRowBytes + (((lane & 15) ^ row_swizzle(r)) * 16)) = vst[i];
+    for (int p = 0; p < kVPass; ++p) {
+      const int r = kRPP * p + lane / kCPR;
+      *(u32x4*)(buf + r * kRB + (((lane % kCPR) ^ row_swizzle(r)) * 16)) = vst[p];
     }
   };
   // V transpose-read offsets (same layout as the flash kernel).
@@ -227,11 +232,11 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
   int voff[2];
 #pragma unroll
   for (int db1 = 0; db1 < 2; ++db1)
-    voff[db1] = (hf * 4 + vr) * kRowBytes + (((4 * db1 + 2 * dh + (vc >> 1)) ^ vsw) * 16) + (vc & 1) * 8;
+    voff[db1] = (hf * 4 + vr) * kRB + (((4 * db1 + 2 * dh + (vc >> 1)) ^ vsw) * 16) + (vc & 1) * 8;
 
-  f32x16 O[4];
+  f32x16 O[kNDB];
 #pragma unroll
-  for (int db = 0; db < 4; ++db) O[db] = f32x16{};
+  for (int db = 0; db < kNDB; ++db) O[db] = f32x16{};
   float m_run = kNegBig, l_run = 0.f;
   const float c2 = a.scale * kLog2e;
 
@@ -246,22 +251,22 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
     }
     f32x16 S = f32x16{};
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) S = mfma32x32x16(kf[ds], qr[ds], S);
+    for (int ds = 0; ds < kNDS; ++ds) S = mfma32x32x16(kf[ds], qr[ds], S);
 
-    // ---- window mask, scores to log2 units.
+    // ---- window mask, scores to log2 units. Score register i of half h2
+    // holds x slot j0 + hf*4 + (i/4)*8 + i%4 of its box row.
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
       const int kb2 = c * kChunk + 16 * h2;
       const int row = kb2 / seg;
       const int j0 = kb2 - row * seg;
-      const int tr = row / ny, yr = row - tr * ny;
+      const int yr = row - (row / ny) * ny;
       const bool row_ok = row < nrows && (unsigned)(yr - sy) < (unsigned)kh;
-      (void)tr;  // every key row of the box is inside the brick's t window
-      const uint64_t xm = row_ok ? (xmask >> (j0 + hf * 4)) : 0ull;
+      // (every key row of the box is inside the brick's t window)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int bit = (i >> 2) * 8 + (i & 3);
-        const bool ok = (xm >> bit) & 1ull;
+        const int jx = j0 + hf * 4 + (i >> 2) * 8 + (i & 3);
+        const bool ok = row_ok && (unsigned)(jx - sx) < (unsigned)kw;
         const float sv = S[8 * h2 + i] * c2;
         S[8 * h2 + i] = ok ? sv : -__builtin_inff();
       }
@@ -278,7 +283,7 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
       m_run = mn;
       l_run *= alpha;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) O[db] *= alpha;
+      for (int db = 0; db < kNDB; ++db) O[db] *= alpha;
     }
     bf16x8 P[2];
 #pragma unroll
@@ -296,27 +301,27 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const unsigned char* base = vb + (16 * j) * kRowBytes + (db >> 1) * 128 + voff[db & 1];
-        const bf16x8 vf = concat(lds_read_tr16(base), lds_read_tr16(base + 8 * kRowBytes));
+      for (int db = 0; db < kNDB; ++db) {
+        const unsigned char* base = vb + (16 * j) * kRB + (db >> 1) * 128 + voff[db & 1];
+        const bf16x8 vf = concat(lds_read_tr16(base), lds_read_tr16(base + 8 * kRB));
         O[db] = mfma32x32x16(vf, P[j], O[db]);
       }
 
     if (has_next) {
       store_v((c & 1) ? vbuf0 : vbuf1);
 #pragma unroll
-      for (int ds = 0; ds < 8; ++ds) kf[ds] = kfn[ds];
+      for (int ds = 0; ds < kNDS; ++ds) kf[ds] = kfn[ds];
     }
   }
 
   const float lt = halves_sum(l_run);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-  u32x4 chunk[4][2];
-  pack_out_rows<4>(O, inv, chunk);  // all lanes: cross-lane exchange
+  u32x4 chunk[kNDB][2];
+  pack_out_rows<kNDB>(O, inv, chunk);  // all lanes: cross-lane exchange
   if (q_in) {
     bf16* orow = og + token(t, yq, xq) * tok_stride;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < kNDB; ++db)
 #pragma unroll
       for (int pr = 0; pr < 2; ++pr) *(u32x4*)(orow + db * 32 + (2 * pr + hf) * 8) = chunk[db][pr];
   }
@@ -874,13 +879,17 @@ int launch_na3d_fwd(const Na3dArgs& a, void* stream, const char** launched) {
       return (int)hipGetLastError();
     }
     case kNaWave: {
-      if (a.D != kD) return (int)hipErrorNotSupported;  // the per-wave kernel is D = 128 only
       const int n_yb = (a.Hs + kBrickY - 1) / kBrickY;
       const int n_xb = (a.W + kBrickX - 1) / kBrickX;
       const int n_xg = (n_xb + kWaves - 1) / kWaves;
       dim3 grid((unsigned)a.T * n_yb * n_xg, a.NH, a.B);
-      hipLaunchKernelGGL(na3d_wave_kernel, grid, dim3(kWaves * 64), 0, st, a, n_yb, n_xb, n_xg);
-      *launched = "na3d_wave_kernel";
+      if (a.D == 128) {
+        hipLaunchKernelGGL((na3d_wave_kernel<128>), grid, dim3(kWaves * 64), 0, st, a, n_yb, n_xb, n_xg);
+        *launched = "na3d_wave_kernel<128>";
+      } else {
+        hipLaunchKernelGGL((na3d_wave_kernel<64>), grid, dim3(kWaves * 64), 0, st, a, n_yb, n_xb, n_xg);
+        *launched = "na3d_wave_kernel<64>";
+      }
       return (int)hipGetLastError();
     }
     default:

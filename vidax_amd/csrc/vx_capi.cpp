@@ -204,7 +204,7 @@ const char* na3d_kernel_label(int32_t variant, int32_t D) {
     case vx::kNaTall: return D == 64 ? "na3d_tall_kernel<64>" : "na3d_tall_kernel<128>";
     case vx::kNaTallWide: return "na3d_tall_wide_kernel<64>";
     case vx::kNaPipe32: return D == 64 ? "na3d_pipe_kernel<32, 64>" : "na3d_pipe_kernel<32, 128>";
-    default: return "na3d_wave_kernel";
+    default: return D == 64 ? "na3d_wave_kernel<64>" : "na3d_wave_kernel<128>";
   }
 }
 
@@ -314,11 +314,6 @@ int32_t na3d_check(const void* q, const void* k, const void* v, const void* out,
     return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 64 and 128)", D);
   if (B > 65535 || NH > 65535)
     return fail(VX_ERR_INVALID_ARGUMENT, "batch (%d) and num_heads (%d) must be <= 65535", B, NH);
-  if ((kw < W ? kw : W) > 57)
-    return fail(VX_ERR_UNSUPPORTED, "kernel_w (clamped to w) = %d exceeds the supported 57", kw < W ? kw : W);
-  if (D == 64 && (kw < W ? kw : W) > 25)
-    return fail(VX_ERR_UNSUPPORTED, "head_dim 64 supports kernel_w (clamped to w) up to 25, got %d",
-                kw < W ? kw : W);
   if (!(scale > 0.f) || !std::isfinite(scale))
     return fail(VX_ERR_INVALID_ARGUMENT, "scale must be positive and finite (got %g)", (double)scale);
   const int64_t tokens = (int64_t)T * Hs * W;
@@ -462,7 +457,7 @@ int32_t injected() {
 
 extern "C" {
 
-int32_t vx_abi_version(void) { return 10500; }
+int32_t vx_abi_version(void) { return 10600; }
 
 const char* vx_last_error(void) { return g_error; }
 
