@@ -48,6 +48,9 @@ WORKLOADS = {
                                                   seed=6),
                                      "3D neighbourhood attention 33x88x160, window (11,11,11), B=1 NH=4 D=64 "
                                      "(LTX-2.5 VAE stage 5 head layout)"),
+    "na3d_wide_x_21x45x80_H24": ("na3d", dict(B=1, T=21, Hs=45, W=80, NH=24, kernel=(3, 7, 31), seed=3),
+                                 "3D neighbourhood attention 21x45x80, window (3,7,31) (x window above 25: the "
+                                 "per-wave kernel), B=1 NH=24 D=128"),
     "na3d_block_fused_q_21x45x80_H24": ("na3d_block", dict(B=1, T=21, Hs=45, W=80, NH=24, kernel=(3, 7, 7), seed=3,
                                                           fused=True),
                                         "NA block attention 21x45x80 (3,7,7) NH=24 D=128: q RMSNorm + "
