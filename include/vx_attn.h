@@ -322,7 +322,8 @@ int32_t vx_rmsnorm_scale_rope_check(const void* x, const void* out, const float*
  * for long key sequences on large grids, else 4 (128-query workgroups), per
  * the library's gfx950 tile table; the environment variable
  * VIDAX_FLASH_BLOCK_SIZES="block_q,block_k_major,block_k" (block_q 128 or
- * 256, key tiles 64) or "default" overrides it. The variable is read once,
+ * 256, key tiles 64) or "default" overrides it. A per-(query, key) bias, or
+ * key_valid together with key_bias, always runs 4 waves. The variable is read once,
  * at the first flash call or plan of the process; a malformed value makes
  * every flash call and plan fail with VX_ERR_INVALID_ARGUMENT, an
  * unsupported one with VX_ERR_UNSUPPORTED.

@@ -263,6 +263,9 @@ def test_flash_kernel_name_follows_the_launch_rule():
     assert flash_kernel_name(1, 200, 200, 4, 64, 4) == "flash_fwd_kernel<4, 64, 4>"
     # a per-(query, key) bias always runs 128-query workgroups
     assert flash_kernel_name(1, 32760, 32760, 40, 128, 5) == "flash_fwd_kernel<5, 128, 4>"
+    # and so does key validity together with a key bias; each alone does not
+    assert flash_kernel_name(1, 32760, 32760, 40, 128, 3) == "flash_fwd_kernel<3, 128, 4>"
+    assert flash_kernel_name(1, 32760, 32760, 40, 128, 2) == "flash_fwd_kernel<2, 128, 8>"
     assert flash_kernel_name(3, 65536, 1025, 1) == "flash_fwd_kernel<0, 128, 8>"      # 768 tiles
 
 

@@ -393,8 +393,9 @@ def test_flash_eight_wave_variants(gpu, D, kind):
     from vidax_amd import _lib, dot_product_attention, flash_attention
     B, Sq, Sk, H = 1, 8192, 1100, 24
     mask_kind = {"plain": 0, "kv_len": 0, "key_valid": 1, "key_bias": 2, "all_key_masks": 3, "full_bias": 5}[kind]
-    # (a per-(query, key) bias always runs 128-query workgroups)
-    name = f"flash_fwd_kernel<{mask_kind}, {D}, {4 if kind == 'full_bias' else 8}>"
+    # (a per-(query, key) bias, and key validity with a key bias, always run
+    # 128-query workgroups)
+    name = f"flash_fwd_kernel<{mask_kind}, {D}, {4 if kind in ('full_bias', 'all_key_masks') else 8}>"
     _say(f"flash 8 waves {name} kind={kind} B={B} Sq={Sq} Sk={Sk} H={H} D={D}")
     seed = 90 + EIGHT_WAVE_KINDS.index(kind) + (0 if D == 128 else 10)
     q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, D, seed)

@@ -229,9 +229,11 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
   // at bias / scale for the lane's keys kb*32 + g*8 + hf*4 + 0..3 of tile j
   // (the tile's mask slot, in LDS by then), so that scale * log2(e) * S is
   // the scaled logit plus bias * log2(e) and bias tiles stay on the fast path.
+  // With a per-(query, key) bias every tile takes the masked path anyway, and
+  // the key bias is added there, next to the full bias (fewer registers).
   const float inv_scale = 1.0f / a.scale;
   auto acc_init = [&](int j, f32x16 (&S)[2]) {
-    if (MASK & kMaskBias) {
+    if ((MASK & kMaskBias) && !kFull) {
       const lds_u8* bslot = lds + kMaskBuf + (j & (kMaskRing - 1)) * kMaskSlot + 64;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -425,6 +427,8 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
             const int kbase = key0 + kb * 32 + g * 8 + hf * 4;
             f32x4 bias = {0.f, 0.f, 0.f, 0.f};
             if (kFull) bias += *(const f32x4*)(frow + kbase) * kLog2e;
+            if (kFull && (MASK & kMaskBias))
+              bias += *(const VX_LDS f32x4*)(mslot + 64 + (kb * 32 + g * 8 + hf * 4) * 4) * kLog2e;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               bool ok = kbase + e < kv_end;
@@ -712,12 +716,14 @@ int launch_one(const FlashArgs& a, hipStream_t stream, const char** launched) {
 }
 
 // The workgroup size (4 or 8 waves) comes from the launch plan in a.waves.
-// (the per-(query, key) bias path always runs 128-query workgroups)
+// (the per-(query, key) bias path, and key validity together with a key
+// bias, always run 128-query workgroups)
 template <int MASK>
 int launch(const FlashArgs& a, hipStream_t stream, const char** launched) {
-  if (a.waves == 4 || (MASK & kMaskFull))
+  constexpr bool kOnly4 = (MASK & kMaskFull) || MASK == (kMaskValid | kMaskBias);
+  if (a.waves == 4 || kOnly4)
     return a.D == 64 ? launch_one<MASK, 4, 64>(a, stream, launched) : launch_one<MASK, 4, 128>(a, stream, launched);
-  if constexpr (!(MASK & kMaskFull))
+  if constexpr (!kOnly4)
     return a.D == 64 ? launch_one<MASK, 8, 64>(a, stream, launched) : launch_one<MASK, 8, 128>(a, stream, launched);
   return (int)hipErrorInvalidValue;
 }

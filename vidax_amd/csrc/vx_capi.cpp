@@ -134,10 +134,14 @@ const FlashTileOverride& tile_override() {
 // Workgroup size for a flash call: the override, else the table's rule. A
 // per-(query, key) bias (the text encoders' short sequences) always runs
 // 128-query workgroups.
-int32_t flash_plan(int32_t B, int32_t Sq, int32_t Sk, int32_t H, bool full_bias, int32_t* waves) {
+// mask_kind bits: 1 key validity, 2 key bias, 4 per-(query, key) bias. The
+// per-(query, key) bias (short text-encoder sequences) and key validity
+// together with a key bias (a rare pair, which needs more registers than
+// the 256-query kernel has without spilling) run 128-query workgroups.
+int32_t flash_plan(int32_t B, int32_t Sq, int32_t Sk, int32_t H, int32_t mask_kind, int32_t* waves) {
   const FlashTileOverride& o = tile_override();
   if (o.rc != VX_OK) return fail(o.rc, "%s", o.error.c_str());
-  if (full_bias) {
+  if ((mask_kind & 4) != 0 || (mask_kind & 3) == 3) {
     *waves = 4;
     return VX_OK;
   }
@@ -266,7 +270,9 @@ int32_t flash_check(const void* q, const void* k, const void* v, const void* out
     return fail(VX_ERR_UNSUPPORTED, "k/v sequence strides (%lld, %lld) above 2^24 elements are not supported",
                 (long long)ks[1], (long long)vs[1]);
   int32_t waves = 0;
-  if ((rc = flash_plan(B, Sq, Sk, H, full_bias != nullptr, &waves)) != VX_OK) return rc;
+  const int32_t mask_kind =
+      (key_valid != nullptr ? 1 : 0) | (key_bias != nullptr ? 2 : 0) | (full_bias != nullptr ? 4 : 0);
+  if ((rc = flash_plan(B, Sq, Sk, H, mask_kind, &waves)) != VX_OK) return rc;
   if (args != nullptr) {
     args->waves = waves;
     args->split_items = 0;
@@ -473,7 +479,7 @@ int32_t vx_flash_attn_split_plan(int32_t batch, int32_t seq_q, int32_t seq_k, in
   if (head_dim != 128 && head_dim != 64)
     return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 64 and 128)", head_dim);
   int32_t waves = 0;
-  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, false, &waves);
+  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, 0, &waves);
   if (rc != VX_OK) return rc;
   const SplitPlan p = flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, waves, num_cus);
   if (split_items != nullptr) *split_items = p.items;
@@ -529,7 +535,7 @@ int32_t vx_flash_attn_plan(int32_t batch, int32_t seq_q, int32_t seq_k, int32_t 
     return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 64 and 128)", head_dim);
   if (mask_kind < 0 || mask_kind > 7) return fail(VX_ERR_INVALID_ARGUMENT, "mask_kind must be in 0..7");
   int32_t waves = 0;
-  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, (mask_kind & 4) != 0, &waves);
+  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, mask_kind, &waves);
   if (rc != VX_OK) return rc;
   flash_kernel_label(mask_kind, head_dim, waves, kernel_name, name_len);
   return ok();
