@@ -529,16 +529,30 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     c.tok = (int64_t)uniform_u64((uint64_t)c.tok);
   };
   const Cursor first = {0, 0, ((int64_t)t_lo * Hs + Y_lo) * W * tok_stride};
-  // Issues the copies of one step (rows c, c+1) and moves c on by kRows rows.
-  auto issue = [&](const bf16* base, int slot_off, Cursor& c) {
-    const int64_t rt0 = c.tok;
+  // The key rows of one step (their token offsets and y in the box), taken
+  // from the cursor, which moves on by kRows rows. K walks the rows; V and
+  // the window mask use each step's record two steps later, so only one
+  // cursor runs (the scalar unit is shared by the CU's 8-16 waves).
+  struct StepRows {
+    int64_t tok0, tok1;
+    int yr0, yr1;
+  };
+  auto next_rows = [&](Cursor& c) -> StepRows {
+    StepRows rr;
+    rr.tok0 = c.tok;
+    rr.yr0 = c.yr;
     advance(c);
-    const int64_t rt1 = C::kRows == 2 ? c.tok : rt0;
+    rr.tok1 = C::kRows == 2 ? c.tok : rr.tok0;
+    rr.yr1 = C::kRows == 2 ? c.yr : rr.yr0;
     if (C::kRows == 2) advance(c);
+    return rr;
+  };
+  // Issues one tensor's copies of one step's rows.
+  auto issue = [&](const bf16* base, int slot_off, const StepRows& rr) {
 #pragma unroll
     for (int p = 0; p < C::kCopiesPerWave; ++p)
       if (C::kCopies % C::kWaves == 0 || wave + C::kWaves * p < C::kCopies)
-        lds_dma16_buf(raw_rsrc(base + (dma_row[p] ? rt1 : rt0)), dma_voff[p], lds_base + slot_off + dma_dst[p]);
+        lds_dma16_buf(raw_rsrc(base + (dma_row[p] ? rr.tok1 : rr.tok0)), dma_voff[p], lds_base + slot_off + dma_dst[p]);
   };
 
   // ---- per-lane LDS offsets (half-plane 0; d 64-127 add kHalfL). K
@@ -591,9 +605,9 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   // ---- prologue: K of steps 0 and 1 in flight, V slot 1 zeroed (it stands
   // in for the V of step -1, paired with P = 0), S = QK^T of chunk 0.
   Cursor kcur = first;  // rows of the next K step to issue
-  Cursor vcur = first;  // rows of the next V step to issue (and of the chunk being masked)
-  issue(kg, C::kK, kcur);
-  issue(kg, C::kK + C::kSlot, kcur);
+  StepRows rows_even = next_rows(kcur), rows_odd = next_rows(kcur);  // steps 0 and 1
+  issue(kg, C::kK, rows_even);
+  issue(kg, C::kK + C::kSlot, rows_odd);
   for (int off = threadIdx.x * 16; off < C::kSlot; off += C::kThreads * 16)
     *(VX_LDS u32x4*)(lds + C::kV + C::kSlot + off) = u32x4{0, 0, 0, 0};
   // q preparation while the first key rows land (its loads overlap theirs)
@@ -607,7 +621,9 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 
   // One step: consumes S (scores of chunk s) and Pp (probabilities of chunk
   // s-1), produces Sn (scores of chunk s+1) and P (probabilities of chunk s).
-  auto step = [&](const int s, f32x16& S, f32x16& Sn, const bf16x8 (&Pp)[2], bf16x8 (&P)[2]) {
+  // rr: the rows of step s on entry (their K was issued two steps ago), the
+  // rows of step s + 2 on return.
+  auto step = [&](const int s, f32x16& S, f32x16& Sn, const bf16x8 (&Pp)[2], bf16x8 (&P)[2], StepRows& rr) {
     // The previous step's copies (K of s+1, V of s-1) have landed once this
     // wave has none outstanding; the barrier publishes everyone's and frees
     // K slot s%2 (K of s, read last step) and V slot s%2 (V of s-2).
@@ -616,17 +632,15 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     // y window of chunk s: whether each of its key rows lies in this lane's
     // window (the x window is in the scores already, as -inf)
     bool row_ok[2];
-    {
-      Cursor c = vcur;
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        if (SEG == 16 && h2 == 1) advance(c);
-        const int r = s * C::kRows + (SEG == 16 ? h2 : 0);
-        row_ok[h2] = r < nrows && (unsigned)(c.yr - sy) < (unsigned)kh;
-      }
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const int r = s * C::kRows + (SEG == 16 ? h2 : 0);
+      row_ok[h2] = r < nrows && (unsigned)((h2 == 0 ? rr.yr0 : rr.yr1) - sy) < (unsigned)kh;
     }
-    issue(kg, C::kK + (s & 1) * C::kSlot, kcur);
-    issue(vg, C::kV + (s & 1) * C::kSlot, vcur);
+    const StepRows cur = rr;
+    rr = next_rows(kcur);
+    issue(kg, C::kK + (s & 1) * C::kSlot, rr);   // K of step s + 2
+    issue(vg, C::kV + (s & 1) * C::kSlot, cur);  // V of step s
 
     const VX_LDS unsigned char* kb = lds + C::kK + ((s + 1) & 1) * C::kSlot;  // K of chunk s+1
     const VX_LDS unsigned char* vb = lds + C::kV + ((s + 1) & 1) * C::kSlot;  // V of chunk s-1
@@ -776,11 +790,11 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   bf16x8 P2[2];
   int s = 0;
   for (; s + 1 < n_steps; s += 2) {
-    step(s, S, S2, Pp, P2);
-    step(s + 1, S2, S, P2, Pp);
+    step(s, S, S2, Pp, P2, rows_even);
+    step(s + 1, S2, S, P2, Pp, rows_odd);
   }
   if (s < n_steps) {
-    step(s, S, S2, Pp, P2);
+    step(s, S, S2, Pp, P2, rows_even);
     Pp[0] = P2[0];
     Pp[1] = P2[1];
   }
