@@ -253,13 +253,21 @@ def test_flash_bias_check():
 
 def test_flash_kernel_name_follows_the_launch_rule():
     """The C ABI's launch plan (gfx950 tile table): 128-query workgroups for
-    key sequences up to 1024 or fewer than 768 256-query tiles, else 256-query.
+    key sequences up to 1024 or fewer than 768 256-query tiles, else 256-query;
+    short key sequences with no key masks but kv_len and at least 4096
+    256-query tiles (at most 64 batch items) run the persistent kernel.
     (The GPU tests check that the launch itself matches the plan.)"""
     from vidax_amd.attention import flash_kernel_name
     assert flash_kernel_name(1, 32760, 32760, 40) == "flash_fwd_kernel<0, 128, 8>"
     assert flash_kernel_name(1, 119056, 119056, 24, 128, 1) == "flash_fwd_kernel<1, 128, 8>"
     assert flash_kernel_name(1, 7800, 7800, 12) == "flash_fwd_kernel<0, 128, 4>"      # 372 tiles
-    assert flash_kernel_name(2, 32760, 512, 40) == "flash_fwd_kernel<0, 128, 4>"      # short keys
+    assert flash_kernel_name(2, 32760, 512, 40) == "flash_stream_kernel<128>"        # short keys, 10240 tiles
+    assert flash_kernel_name(2, 32760, 512, 40, 64) == "flash_stream_kernel<64>"
+    assert flash_kernel_name(1, 65536, 1024, 16) == "flash_stream_kernel<128>"       # 4096 tiles
+    assert flash_kernel_name(1, 65536, 1025, 16) == "flash_fwd_kernel<0, 128, 8>"    # keys above 1024
+    assert flash_kernel_name(1, 65280, 1024, 16) == "flash_fwd_kernel<0, 128, 4>"    # 4080 tiles
+    assert flash_kernel_name(65, 4096, 512, 4) == "flash_fwd_kernel<0, 128, 4>"      # 65 batch items
+    assert flash_kernel_name(2, 32760, 512, 40, 128, 1) == "flash_fwd_kernel<1, 128, 4>"  # key validity
     assert flash_kernel_name(1, 200, 200, 4, 64, 4) == "flash_fwd_kernel<4, 64, 4>"
     # a per-(query, key) bias always runs 128-query workgroups
     assert flash_kernel_name(1, 32760, 32760, 40, 128, 5) == "flash_fwd_kernel<5, 128, 4>"
@@ -334,11 +342,11 @@ _PLANS = ("from vidax_amd import _lib\n"
 
 
 @pytest.mark.parametrize("value,expect", [
-    (None, ["flash_fwd_kernel<0, 128, 8>", "flash_fwd_kernel<0, 128, 4>", "flash_fwd_kernel<0, 128, 4>"]),
-    ("default", ["flash_fwd_kernel<0, 128, 8>", "flash_fwd_kernel<0, 128, 4>", "flash_fwd_kernel<0, 128, 4>"]),
-    (" DEFAULT ", ["flash_fwd_kernel<0, 128, 8>", "flash_fwd_kernel<0, 128, 4>", "flash_fwd_kernel<0, 128, 4>"]),
+    (None, ["flash_fwd_kernel<0, 128, 8>", "flash_stream_kernel<128>", "flash_fwd_kernel<0, 128, 4>"]),
+    ("default", ["flash_fwd_kernel<0, 128, 8>", "flash_stream_kernel<128>", "flash_fwd_kernel<0, 128, 4>"]),
+    (" DEFAULT ", ["flash_fwd_kernel<0, 128, 8>", "flash_stream_kernel<128>", "flash_fwd_kernel<0, 128, 4>"]),
     ("128,64,64", ["flash_fwd_kernel<0, 128, 4>"] * 3),
-    ("256, 64, 64", ["flash_fwd_kernel<0, 128, 8>"] * 3),
+    ("256, 64, 64", ["flash_fwd_kernel<0, 128, 8>", "flash_stream_kernel<128>", "flash_fwd_kernel<0, 128, 8>"]),
 ])
 def test_flash_block_sizes_override(value, expect):
     """VIDAX_FLASH_BLOCK_SIZES (the reference's override, core/attention.py:

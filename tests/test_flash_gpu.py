@@ -240,7 +240,9 @@ def test_flash_config3_cross_kvlen(gpu):
     _say("flash c3 cross B=2 H=40 Lq=32760 Lk=512 kv_len")
     q, k, v = _torch_inputs(2, 32760, 512, 40, 2, gpu)
     kv_len = np.random.default_rng(2).integers(20, 513, size=2).astype(np.int32)
+    from vidax_amd import _lib
     out = flash_attention(q, k, v, kv_len=torch.from_numpy(kv_len).to(gpu))
+    assert _lib.last_launch() == "flash_stream_kernel<128>", _lib.last_launch()
     rows = _rows(32760, 512, 2)
     ref = O.attention_rows(_np(q), _np(k), _np(v), rows, kv_len=kv_len)
     _check(out[:, torch.from_numpy(rows).to(gpu)], ref, "c3 rows")
@@ -560,6 +562,68 @@ def test_flash_forced_block_sizes(gpu, block_q, shape):
     assert r["name"] in (f"flash_fwd_kernel<0, {shape[4]}, {block_q // 32}>",
                          f"flash_fwd_split_kernel<0, {shape[4]}, {block_q // 32}>"), r["name"]
     assert r["max"] <= MAX_ABS and r["mean"] <= MEAN_ABS
+
+
+# ------------------------------------------- persistent short-key kernel
+STREAM_CASES = [
+    # B, Sq, Sk, H, D, kv_len, seed
+    (2, 32768, 512, 16, 128, [432, 148], 160),   # seven- and three-tile items (the cross-attention mix)
+    (3, 15000, 300, 24, 128, [0, 65, 300], 161), # an empty batch item, two-tile items, ragged queries
+    (2, 20000, 130, 26, 128, [1, 64], 162),      # one-tile items
+    (1, 65536, 1024, 16, 128, None, 163),        # sixteen tiles, no kv_len
+    (2, 32760, 512, 16, 64, [512, 20], 164),     # head dim 64
+]
+
+
+@pytest.mark.parametrize("B,Sq,Sk,H,D,kv,seed", STREAM_CASES)
+def test_flash_stream_kernel(gpu, B, Sq, Sk, H, D, kv, seed):
+    """The persistent short-key kernel (one workgroup per CU running the key
+    tiles of its items as one stream): rows at every position of a 256-query
+    tile, and the first and last rows, against the oracle (zero rows for
+    kv_len 0); and bit for bit the output of the 128-query kernel given the
+    same keys as a boolean key mask."""
+    from vidax_amd import _lib, dot_product_attention, flash_attention
+    _say(f"flash stream B={B} Sq={Sq} Sk={Sk} H={H} D={D} kv_len={kv} seed={seed}")
+    g = torch.Generator(device=gpu)
+    g.manual_seed(seed)
+    q, k, v = (torch.randn((B, n, H, D), generator=g, device=gpu, dtype=torch.float32).to(torch.bfloat16)
+               for n in (Sq, Sk, Sk))
+    kv_t = None if kv is None else torch.tensor(kv, dtype=torch.int32, device=gpu)
+    out = flash_attention(q, k, v, kv_len=kv_t)
+    torch.cuda.synchronize()
+    assert _lib.last_launch() == f"flash_stream_kernel<{D}>", _lib.last_launch()
+    rows = _residue_rows(Sq, 1, seed)
+    kv_np = None if kv is None else np.array(kv, np.int32)
+    ref = O.attention_rows(_np(q), _np(k), _np(v), rows, kv_len=kv_np)
+    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, "stream rows")
+    if kv is not None:
+        valid = torch.arange(Sk, device=gpu)[None, :] < kv_t[:, None]
+        out2 = dot_product_attention(q, k, v, mask=valid[:, None, None, :])
+        torch.cuda.synchronize()
+        assert _lib.last_launch() == f"flash_fwd_kernel<1, {D}, 4>", _lib.last_launch()
+        assert torch.equal(out, out2)
+
+
+def test_flash_stream_kernel_strided_views(gpu):
+    """q, k and v as views into wider rows (the persistent kernel's copies
+    use each tensor's own strides)."""
+    from vidax_amd import _lib, flash_attention
+    _say("flash stream strided views B=2 Sq=20000 Sk=200 H=26")
+    B, Sq, Sk, H, D = 2, 20000, 200, 26, 128
+    g = torch.Generator(device=gpu)
+    g.manual_seed(165)
+    qw = torch.randn((B, Sq, H, 2 * D), generator=g, device=gpu, dtype=torch.float32).to(torch.bfloat16)
+    kvw = torch.randn((B, Sk, 3, H, D), generator=g, device=gpu, dtype=torch.float32).to(torch.bfloat16)
+    q, k, v = qw[..., D:], kvw[:, :, 0], kvw[:, :, 2]
+    kv = np.array([200, 77], np.int32)
+    out = flash_attention(q, k, v, kv_len=torch.from_numpy(kv).to(gpu))
+    torch.cuda.synchronize()
+    assert _lib.last_launch() == "flash_stream_kernel<128>", _lib.last_launch()
+    rows = _residue_rows(Sq, 1, 165)
+    ref = O.attention_rows(_np(q), _np(k), _np(v), rows, kv_len=kv)
+    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, "stream strided rows")
+    out_c = flash_attention(q.contiguous(), k.contiguous(), v.contiguous(), kv_len=torch.from_numpy(kv).to(gpu))
+    assert torch.equal(out, out_c)
 
 
 # ------------------------------------------------ key split of the last round

@@ -33,6 +33,7 @@
 #include "vx_gfx950.hpp"
 #include "vx_kernels.h"
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 
@@ -91,6 +92,7 @@ static_assert(kSumLimit == (float)(1 << (int)kRescaleSlack), "the tile-sum limit
 constexpr float kNegBig = -1.0e30f;           // finite "no key seen yet" max
 
 typedef VX_LDS unsigned char lds_u8;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 // One workgroup's work: query tile `qtile` of (head, b) over the keys
 // [k_lo, k_hi) (k_lo a multiple of the key tile). part < 0 writes the
@@ -679,6 +681,595 @@ __global__ __launch_bounds__(WAVES * 64) void flash_combine_kernel(const FlashAr
   }
 }
 
+// ---- persistent kernel for short key sequences (key masks: kv_len only).
+//
+// One 8-wave workgroup per CU. Each workgroup takes a contiguous range of
+// (256-query tile, head, batch item) items, the ranges cut so that every
+// workgroup gets about the same number of key tiles (each item counted with
+// one tile more for its start and end), and runs the key tiles of its items
+// as one stream u = 0, 1, ...: step u takes the softmax of stream tile u,
+// PV of tile u-1 and QK^T of tile u+1 in its MFMA slots, and copies K_{u+3}
+// and V_{u+1}, whichever items these tiles belong to. So the next item's
+// first tiles are copied while the current item ends; the QK^T slots of an
+// item's last step score the next item's first tile (its q tile was copied
+// into LDS at the item's first step and is read into registers at the top
+// of that last step); and the PV slots of an item's first step finish the
+// previous item, whose output rows are stored at the end of that step. The
+// 256-query items copy half the K/V bytes per query of 128-query
+// workgroups, and the stream takes each item's pipeline fill and drain
+// (q load, first copies, last PV and stores) off the critical path.
+// Workgroup g runs on XCD g % 8 (round-robin dispatch), and the XCDs take
+// contiguous eighths of the items, so that each XCD's L2 holds the K/V of
+// few heads. Items of a batch item with kv_len 0 get zero rows.
+template <int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void flash_stream_kernel(const FlashArgs a) {
+  using C = FCfg<D, 8>;
+  constexpr int kWaves = 8, kThreads = 512;
+  constexpr int kTileBytes = C::kTileBytes;
+  constexpr int kLoadsPerWave = C::kLoadsPerWave, kCopyWaves = C::kCopyWaves;
+  constexpr int kDB = C::kDB, kDS = C::kDS, kPV = C::kPV, kSlots = C::kSlots;
+  // LDS: two V tiles (V_u is copied in step u and read in step u+1), three
+  // K tiles (K_{u+3} copied in step u, read in step u+2), the next item's q
+  // tile (four 64-row tiles in the K layout) and the table of the
+  // workgroup's items (kTabMax entries of 16 bytes: batch item, head, query
+  // tile, keys; the launcher keeps every workgroup within it)
+  constexpr int kKNB = 3;
+  constexpr int kVBuf = 0, kKBuf = 2 * kTileBytes, kQBuf = 5 * kTileBytes, kTab = 9 * kTileBytes;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kTab + kStreamTabMax * 16];
+  lds_u8* const lds = (lds_u8*)smem;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hf = lane >> 5, col = lane & 31;
+  const int n_qt = (a.Sq + 255) / 256;
+  const int per_b = a.H * n_qt;  // items per batch item
+  auto uni = [](int x) { return __builtin_amdgcn_readfirstlane(x); };
+  auto kv_end_of = [&](int b) -> int {
+    int kv = a.Sk;
+    if (a.kv_len != nullptr) kv = min(max(a.kv_len[b], 0), a.Sk);
+    return uni(kv);
+  };
+  auto tiles_of = [](int kv) { return (kv + kBN - 1) / kBN; };
+
+  // ---- this workgroup's items [i_lo, i_hi): item j of batch item b starts
+  // at work P_b + j * (n_b + 1), P_b the work of the batch items before b
+  int64_t W = 0;
+  for (int b = 0; b < a.B; ++b) W += (int64_t)per_b * (tiles_of(kv_end_of(b)) + 1);
+  const int G = gridDim.x;
+  const int chunk_id = (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8;
+  auto first_item_at = [&](int64_t x) -> int {  // first item starting at or after work x
+    int64_t P = 0;
+    for (int b = 0; b < a.B; ++b) {
+      const int w = tiles_of(kv_end_of(b)) + 1;
+      const int64_t end = P + (int64_t)per_b * w;
+      if (x < end) return b * per_b + (int)((x - P + w - 1) / w);
+      P = end;
+    }
+    return a.B * per_b;
+  };
+  const int i_lo = uni(first_item_at(W * chunk_id / G));
+  const int i_hi = uni(first_item_at(W * (chunk_id + 1) / G));
+
+  // stream length; items of batch items with no keys get zero rows
+  int U = 0;
+  for (int b = i_lo / per_b; b < a.B && b * per_b < i_hi; ++b) {
+    const int lo = max(i_lo, b * per_b), hi = min(i_hi, (b + 1) * per_b);
+    const int n = tiles_of(kv_end_of(b));
+    U += (hi - lo) * n;
+    if (n == 0) {
+      for (int i = lo; i < hi; ++i) {
+        const int r = i - b * per_b, h = r / n_qt, qi = (r % n_qt * kWaves + wave) * 32 + col;
+        if (qi < a.Sq) {
+          bf16* orow = (bf16*)a.o + (b * a.os[0] + h * a.os[2]) + (int64_t)qi * a.os[1];
+#pragma unroll
+          for (int db = 0; db < kDB; ++db)
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) *(u32x4*)(orow + db * 32 + (2 * pr + hf) * 8) = u32x4{0, 0, 0, 0};
+        }
+      }
+    }
+  }
+  U = uni(U);
+  if (U == 0) return;
+
+  // ---- the table of this workgroup's items with keys (built by all
+  // threads; entry e of the items in [i_lo, i_hi) minus those of batch items
+  // without keys before it)
+  int n_items = 0;
+  for (int b = i_lo / per_b; b < a.B && b * per_b < i_hi; ++b)
+    if (kv_end_of(b) > 0) n_items += min(i_hi, (b + 1) * per_b) - max(i_lo, b * per_b);
+  n_items = uni(n_items);
+  for (int e = threadIdx.x; e < i_hi - i_lo; e += kThreads) {
+    const int i = i_lo + e, b = i / per_b;
+    const int kv = a.kv_len != nullptr ? min(max(a.kv_len[b], 0), a.Sk) : a.Sk;
+    if (kv == 0) continue;
+    int skip = 0;
+    for (int bb = i_lo / per_b; bb < b; ++bb) {
+      const int kvb = a.kv_len != nullptr ? min(max(a.kv_len[bb], 0), a.Sk) : a.Sk;
+      if (kvb == 0) skip += min(i_hi, (bb + 1) * per_b) - max(i_lo, bb * per_b);
+    }
+    const int r = i - b * per_b, h = r / n_qt;
+    if (e - skip < kStreamTabMax)  // (always: the launcher sizes the grid so)
+      *(VX_LDS i32x4*)(lds + kTab + (e - skip) * 16) = i32x4{b, h, r - h * n_qt, kv};
+  }
+  __syncthreads();
+  struct Item {
+    int b, h, qt, kv;
+  };
+  auto entry = [&](int e) -> Item {
+    const i32x4 v = *(const VX_LDS i32x4*)(lds + kTab + e * 16);
+    return Item{uni(v[0]), uni(v[1]), uni(v[2]), uni(v[3])};
+  };
+
+  // ---- LDS offsets (the layout of flash_tile: half-planes of 64 rows x
+  // 128 bytes, 16-byte chunks XOR-swizzled per row)
+  // K fragment (kb, ds): key kb*32 + col, chunk 2*(ds%4) + hf of half ds/4,
+  // at koff0 ^ ((ds % 4) << 5) (2*(ds%4) + hf = 2*(ds%4) ^ hf). Inside the
+  // key loop the offsets (and the V ones derived from voff) are formed at
+  // each use from values made opaque by an empty asm, so that they do not
+  // hold registers across the whole loop, which has none to spare.
+  const int koff0 = col * 128 + ((hf ^ half_swizzle(col)) * 16);
+  auto kofs = [&](int d4) { return koff0 ^ (d4 << 5); };
+  auto kofs_loop = [&](int d4) {
+    int k = koff0;
+    asm volatile("" : "+v"(k));
+    return k ^ (d4 << 5);
+  };
+  const int i16 = lane & 15;
+  const int vr = i16 >> 2, vc4 = i16 & 3, dh = (lane >> 4) & 1;
+  int voff[2];
+#pragma unroll
+  for (int db1 = 0; db1 < 2; ++db1) {
+    const int key = hf * 4 + vr;
+    voff[db1] = key * 128 + (((4 * db1 + 2 * dh + (vc4 >> 1)) ^ half_swizzle(key)) * 16) + (vc4 & 1) * 8;
+  }
+  const int srow = lane >> 3, scol = lane & 7;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+  struct Lanes {
+    uint32_t k[kLoadsPerWave], v[kLoadsPerWave];
+  };
+  auto make_lanes = [&]() {
+    Lanes ln;
+#pragma unroll
+    for (int p = 0; p < kLoadsPerWave; ++p) {
+      const int i = (wave % kCopyWaves) * kLoadsPerWave + p;
+      const int r = 8 * (i & 7) + srow;
+      const int col_el = (i >> 3) * 64 + ((scol ^ half_swizzle(r)) * 8);
+      ln.k[p] = (uint32_t)(r * (int)a.ks[1] + col_el) * 2u;
+      ln.v[p] = (uint32_t)(r * (int)a.vs[1] + col_el) * 2u;
+    }
+    return ln;
+  };
+  const uint64_t q_addr = uniform_u64((uint64_t)(uintptr_t)a.q);
+  const uint64_t k_addr = uniform_u64((uint64_t)(uintptr_t)a.k);
+  const uint64_t v_addr = uniform_u64((uint64_t)(uintptr_t)a.v);
+  const uint64_t k_tile_bytes = uniform_u64((uint64_t)a.ks[1] * (2 * kBN));
+  const uint64_t v_tile_bytes = uniform_u64((uint64_t)a.vs[1] * (2 * kBN));
+  // this wave's copies of 64 rows from byte address `addr` into the LDS tile
+  // at buf_off; rows from rows_left on repeat row rows_left - 1 (>= 0)
+  // (the per-lane terms are formed at each call: an empty asm on the lane
+  // index keeps them out of the registers of the whole key loop)
+  auto stage_clamped = [&](uint64_t addr, int64_t stride, int rows_left, int buf_off) {
+    const i32x4_rsrc rs = raw_rsrc_u64(addr);
+    const uint32_t dst = lds_base + buf_off + (uint32_t)(wave * kLoadsPerWave) * 1024u;
+    int ln_ = lane;
+    asm volatile("" : "+v"(ln_));
+    const int sr = ln_ >> 3, sc = ln_ & 7;
+#pragma unroll
+    for (int p = 0; p < kLoadsPerWave; ++p) {
+      const int i = wave * kLoadsPerWave + p;
+      const int r = 8 * (i & 7) + sr;
+      const int rr = min(r, rows_left - 1);
+      const uint32_t off = (uint32_t)(rr * (int)stride + (i >> 3) * 64 + ((sc ^ half_swizzle(r)) * 8)) * 2u;
+      lds_dma16_buf(rs, off, dst + p * 1024);
+    }
+  };
+  auto stage_rows = [&](uint64_t addr, const uint32_t (&lanep)[kLoadsPerWave], int64_t stride, int rows_left,
+                        int buf_off) {
+    if (rows_left >= kBN) {
+      const i32x4_rsrc rs = raw_rsrc_u64(addr);
+      const uint32_t dst = lds_base + buf_off + (uint32_t)(wave * kLoadsPerWave) * 1024u;
+#pragma unroll
+      for (int p = 0; p < kLoadsPerWave; ++p) lds_dma16_buf(rs, lanep[p], dst + p * 1024);
+    } else {
+      stage_clamped(addr, stride, rows_left, buf_off);
+    }
+  };
+  // q rows of table entry e (4 x 64 rows; rows past Sq repeat row Sq - 1)
+  auto stage_q = [&](int e) {
+    const Item it = entry(e);
+    const uint64_t head = q_addr + (uint64_t)((int64_t)it.b * a.qs[0] + (int64_t)it.h * a.qs[2]) * 2u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r0 = min(it.qt * 256 + 64 * j, a.Sq - 1);
+      stage_clamped(head + (uint64_t)((int64_t)r0 * a.qs[1]) * 2u, a.qs[1], a.Sq - r0, kQBuf + j * kTileBytes);
+    }
+  };
+  // this wave's 32 q rows from the q buffer (the B operand of QK^T)
+  auto load_q = [&](bf16x8 (&qr)[kDS]) {
+    const lds_u8* qb = lds + kQBuf + (wave >> 1) * kTileBytes + (wave & 1) * 32 * 128;
+#pragma unroll
+    for (int ds = 0; ds < kDS; ++ds)
+      qr[ds] = *(const VX_LDS bf16x8*)(qb + kofs_loop(ds & 3) + (ds >> 2) * C::kHalfBytes);
+  };
+
+  // ---- copy cursors (wave-uniform): byte address of the tile's first row,
+  // its rows below kv_end, the tiles left in its item, its table entry.
+  // After the stream's last tile a cursor stays there (that tile is copied
+  // again).
+  struct CopyCur {
+    uint64_t addr;
+    int rows, left, e;
+  };
+  auto open_copy = [&](CopyCur& c, int e, uint64_t base, const int64_t (&s)[3]) {
+    const Item it = entry(e);
+    c.e = e;
+    c.rows = it.kv;
+    c.left = tiles_of(it.kv);
+    c.addr = uniform_u64(base + (uint64_t)((int64_t)it.b * s[0] + (int64_t)it.h * s[2]) * 2u);
+  };
+  auto advance_copy = [&](CopyCur& c, uint64_t base, const int64_t (&s)[3], uint64_t tile_bytes) {
+    if (c.left > 1) {
+      --c.left;
+      c.rows -= kBN;
+      c.addr += tile_bytes;
+      return;
+    }
+    if (c.e + 1 < n_items) open_copy(c, c.e + 1, base, s);
+  };
+
+  // ---- the scored tile (wave-uniform): table entry, tile in it, its tiles
+  // and keys
+  int c_e = 0;
+  int c_kv = entry(0).kv;
+  int c_n = tiles_of(c_kv), c_t = 0;
+  bool has_prev = false;
+
+  const float c = a.scale * kLog2e;
+  f32x16 O[kDB];
+#pragma unroll
+  for (int db = 0; db < kDB; ++db) O[db] = f32x16{};
+  float m_run = kNegBig, l_run = 0.f;
+
+  // output rows of table entry e, normalised by the row sum l (one 32-wide
+  // d block at a time: few registers, as it runs inside the key loop).
+  // Lanes past Sq hold row Sq-1's query (the q copies repeat that row), so
+  // they store row Sq-1's output again, the same bytes: every wave issues
+  // exactly 2 * kDB stores, which the copying waves' waits count.
+  auto epilogue = [&](int e, float l) {
+    const float lt = halves_sum(l);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    const Item it = entry(e);
+    int ln_ = lane;
+    asm volatile("" : "+v"(ln_));
+    const int qi = (it.qt * kWaves + wave) * 32 + (ln_ & 31);
+    bf16* orow = (bf16*)a.o + (it.b * a.os[0] + it.h * a.os[2]) + (int64_t)min(qi, a.Sq - 1) * a.os[1];
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) {
+      u32x4 chunk[1][2];
+      const f32x16 Ob[1] = {O[db]};
+      pack_out_rows<1>(Ob, inv, chunk);
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) *(u32x4*)(orow + db * 32 + (2 * pr + (ln_ >> 5)) * 8) = chunk[0][pr];
+    }
+  };
+  auto probs = [&](const f32x16 (&S)[2], float cc_, float m, bf16x8 (&P)[2][2]) -> float {
+    const float mneg = -m;
+    float l = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        bf16x8 pv8;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) pv8[r] = (bf16)fast_exp2(__builtin_fmaf(S[kb][8 * j + r], cc_, mneg));
+        P[kb][j] = pv8;
+        l = sum8(pv8, l);
+      }
+    return l;
+  };
+
+  // ---- prologue: q of the first item, K_0..K_2; V buffer 1 is "V_{-1}"
+  // (zeros, paired with P = 0 in step 0)
+  CopyCur kc{}, vc{};
+  bf16x8 qr[kDS];
+  if (wave < kCopyWaves) {
+    const Lanes ln = make_lanes();
+    open_copy(kc, 0, k_addr, a.ks);
+    open_copy(vc, 0, v_addr, a.vs);
+    stage_q(0);
+#pragma unroll
+    for (int j = 0; j < kKNB; ++j) {
+      stage_rows(kc.addr, ln.k, a.ks[1], kc.rows, kKBuf + j * kTileBytes);
+      advance_copy(kc, k_addr, a.ks, k_tile_bytes);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < kTileBytes / (kThreads * 16); ++p)
+    *(VX_LDS u32x4*)(lds + kVBuf + kTileBytes + (p * kThreads + threadIdx.x) * 16) = u32x4{0, 0, 0, 0};
+  // Step u copies V_u, then K_{u+3}: at its top, V_{u-1} (the previous
+  // step's first copies) and K_{u+1} have landed; the previous step's K copy
+  // may still be in flight, and so may the output stores issued after it
+  // (`stored`: the previous step ended an item). Only the copying waves
+  // wait; the barrier after the wait publishes their copies to all waves.
+  bool stored = false;
+  auto wait_prev = [&]() {
+    if (wave < kCopyWaves) {
+      if (stored)
+        wait_vmem<kLoadsPerWave + 2 * kDB>();
+      else
+        wait_vmem<kLoadsPerWave>();
+    }
+  };
+  wait_prev();
+  __syncthreads();
+  load_q(qr);
+  f32x16 S[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+  for (int ds = 0; ds < kDS; ++ds)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const bf16x8 kf = *(const VX_LDS bf16x8*)(lds + kKBuf + kofs(ds & 3) + kb * 32 * 128 + (ds >> 2) * C::kHalfBytes);
+      S[kb] = mfma32x32x16(kf, qr[ds], S[kb]);
+    }
+  bf16x8 Pp[2][2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) Pp[kb][j] = bf16x8{};
+
+  int kb_cur = 1;   // K buffer holding K_{u+1}
+  int vb_prev = 1;  // V buffer holding V_{u-1}
+  // Stream step u (flash_tile's step; the item changes happen between
+  // steps, below): consumes S (scores of tile u) and Pp (probabilities of
+  // tile u-1), produces Sn (scores of tile u+1) and P (probabilities of tile
+  // u); returns the row sum of P (this lane's part).
+  auto step = [&](auto copy_tag, const Lanes& ln, const int u, f32x16 (&S)[2], f32x16 (&Sn)[2],
+                  const bf16x8 (&Pp)[2][2], bf16x8 (&P)[2][2]) __attribute__((always_inline)) -> float {
+    constexpr bool COPY = decltype(copy_tag)::value;
+    const bool first = c_t == 0;
+    wait_prev();
+    __syncthreads();
+    const int kb_next = kb_cur == 0 ? kKNB - 1 : kb_cur - 1;  // u % 3
+    const int key0 = c_t * kBN;
+    const bool slow = key0 + kBN > c_kv;
+    if (COPY) {
+      // the next item's q (items of two or more tiles) first: the waits
+      // count the tile copies after it
+      if (first && c_n > 1 && u + c_n < U) stage_q(c_e + 1);
+      stage_rows(vc.addr, ln.v, a.vs[1], vc.rows, kVBuf + (vb_prev ^ 1) * kTileBytes);
+      advance_copy(vc, v_addr, a.vs, v_tile_bytes);
+      stage_rows(kc.addr, ln.k, a.ks[1], kc.rows, kKBuf + kb_next * kTileBytes);
+      advance_copy(kc, k_addr, a.ks, k_tile_bytes);
+    }
+    float cc_ = c;
+    if (slow) {  // the item's tail tile: keys from kv_end on -> -inf
+      cc_ = 1.0f;
+      int ln_ = lane;
+      asm volatile("" : "+v"(ln_));
+      const int hf4 = (ln_ >> 5) * 4;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int kbase = key0 + kb * 32 + g * 8 + hf4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float sv = S[kb][g * 4 + e] * c;
+            S[kb][g * 4 + e] = kbase + e < c_kv ? sv : -__builtin_inff();
+          }
+        }
+    }
+
+    float l_tile = 0.f, alpha = 1.f;
+    bool rare = false;
+    {
+      const lds_u8* kb0 = lds + kKBuf + kb_cur * kTileBytes;
+      const lds_u8* vb0 = lds + kVBuf + vb_prev * kTileBytes;
+      auto frag = [&](int s) -> bf16x8 {
+        if (s < kPV) {
+          const int db = s % kDB, j = (s / kDB) & 1, kb = s / (2 * kDB);
+          const lds_u8* p = vb0 + (kb * 32 + 16 * j) * 128 + (db >> 1) * C::kHalfBytes;
+          int vo = voff[db & 1];
+          asm volatile("" : "+v"(vo));
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + vo));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + 8 * 128 + (vo ^ 16)));
+          return concat(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi));
+        }
+        const int ds = (s - kPV) >> 1, kb = (s - kPV) & 1;
+        return *(const VX_LDS bf16x8*)(kb0 + kofs_loop(ds & 3) + kb * 32 * 128 + (ds >> 2) * C::kHalfBytes);
+      };
+      const bf16x2 one2 = {(bf16)1.0f, (bf16)1.0f};
+      if (!COPY) __builtin_amdgcn_s_setprio(1);
+      bf16x8 fr[kSlots];
+      float pf[32];
+      bf16x2 pk[16];
+      fr[0] = frag(0);
+      fr[1] = frag(1);
+      fr[2] = frag(2);
+      auto softmax_block = [&]() {
+        const float mneg = -m_run;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) pf[8 * g + i] = __builtin_fmaf(S[g >> 1][8 * (g & 1) + i], cc_, mneg);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) pf[8 * g + i] = fast_exp2(pf[8 * g + i]);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pk[4 * g + i] = bf16x2{(bf16)pf[8 * g + 2 * i], (bf16)pf[8 * g + 2 * i + 1]};
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[i], one2, l_tile, false);
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      auto pack_p = [&]() {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int q = kb * 8 + j * 4;
+            P[kb][j] = __builtin_shufflevector(__builtin_shufflevector(pk[q], pk[q + 1], 0, 1, 2, 3),
+                                               __builtin_shufflevector(pk[q + 2], pk[q + 3], 0, 1, 2, 3),
+                                               0, 1, 2, 3, 4, 5, 6, 7);
+          }
+      };
+      // rare path (not an item's first tile): the tile's probabilities
+      // against its max, O and l_run rescaled to it. The copying waves take
+      // it before their slots (the scores are then dead during the slots,
+      // which keeps the kernel within its registers) and rescale O after
+      // them; the results are the same.
+      auto rare_path = [&]() {
+        if (__builtin_amdgcn_ballot_w64(l_tile > kSumLimit || is_nan_bits(l_tile)) != 0) {
+          rare = true;
+          float mxc = -__builtin_inff();
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mxc = __builtin_fmaxf(__builtin_fmaxf(mxc, S[0][e]), S[1][e]);
+          const float mn = fmaxf(m_run, halves_max(mxc) * cc_);
+          alpha = fast_exp2(m_run - mn);
+          m_run = mn;
+          l_run *= alpha;
+          if (!COPY) {
+#pragma unroll
+            for (int db = 0; db < kDB; ++db) O[db] *= alpha;
+          }
+          l_tile = probs(S, cc_, m_run, P);
+        }
+      };
+      // an item's first tile takes its max first (m_run = the rare path's
+      // reference point for it), so that the speculative pass stands
+      auto tile_probs = [&]() {
+        if (first) {
+          float mxc = -__builtin_inff();
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mxc = __builtin_fmaxf(__builtin_fmaxf(mxc, S[0][e]), S[1][e]);
+          m_run = fmaxf(kNegBig, halves_max(mxc) * cc_);
+        }
+        softmax_block();
+        pack_p();
+        rare_path();
+      };
+      if (COPY) tile_probs();
+      Sn[0] = f32x16{};
+      Sn[1] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < kSlots; ++s) {
+        if (s + 3 < kSlots) fr[s + 3] = frag(s + 3);
+        if (s < kPV) {
+          const int db = s % kDB, j = (s / kDB) & 1, kb = s / (2 * kDB);
+          O[db] = mfma32x32x16(fr[s], Pp[kb][j], O[db]);
+        } else {
+          const int ds = (s - kPV) >> 1, kb = (s - kPV) & 1;
+          Sn[kb] = mfma32x32x16(fr[s], qr[ds], Sn[kb]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (!COPY) __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (!COPY) tile_probs();
+    }
+    if (COPY && rare) {
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) O[db] *= alpha;
+    }
+    kb_cur = kb_cur == kKNB - 1 ? 0 : kb_cur + 1;
+    vb_prev ^= 1;
+    return l_tile;
+  };
+  // Step u with the item changes around it: an item's first step resets the
+  // reference point (and a one-tile item copies and loads the next item's q
+  // first: its own QK^T slots score that item); after it, the previous
+  // item's rows are stored and O restarts; after the step that scored the
+  // item's last tile, the next item's q is loaded for the next step's slots.
+  auto stream_step = [&](auto copy_tag, const Lanes& ln, const int u, f32x16 (&S)[2], f32x16 (&Sn)[2],
+                         const bf16x8 (&Pp)[2][2], bf16x8 (&P)[2][2]) __attribute__((always_inline)) {
+    constexpr bool COPY = decltype(copy_tag)::value;
+    const bool first = c_t == 0, last = c_t + 1 == c_n;
+    if (first) {
+      if (c_n == 1 && u + 1 < U) {
+        if (COPY) {
+          stage_q(c_e + 1);
+          wait_vmem<0>();
+        }
+        __syncthreads();
+        load_q(qr);
+      }
+    }
+    const float l_tile = step(copy_tag, ln, u, S, Sn, Pp, P);
+    stored = first && has_prev;
+    if (first) {
+      if (has_prev) epilogue(c_e - 1, l_run);
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) O[db] = f32x16{};
+      l_run = l_tile;
+    } else {
+      l_run += l_tile;
+    }
+    if (c_t + 2 == c_n && u + 2 < U) {
+      // (a two-tile item copied the next item's q in this step)
+      if (first) {
+        if (COPY) wait_vmem<0>();
+        __syncthreads();
+      }
+      load_q(qr);
+    }
+    if (!last) {
+      ++c_t;
+    } else if (u + 1 < U) {
+      has_prev = true;
+      ++c_e;
+      c_kv = entry(c_e).kv;
+      c_n = tiles_of(c_kv);
+      c_t = 0;
+    }
+  };
+
+  f32x16 S2[2];
+  bf16x8 P2[2][2];
+  auto stream_loop = [&](auto copy_tag) __attribute__((always_inline)) {
+    Lanes ln{};
+    if constexpr (decltype(copy_tag)::value) ln = make_lanes();
+    int u = 0;
+    for (; u + 1 < U; u += 2) {
+      stream_step(copy_tag, ln, u, S, S2, Pp, P2);
+      stream_step(copy_tag, ln, u + 1, S2, S, P2, Pp);
+    }
+    if (u < U) {
+      stream_step(copy_tag, ln, u, S, S2, Pp, P2);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) Pp[kb][j] = P2[kb][j];
+    }
+  };
+  if (wave < kCopyWaves)
+    stream_loop(std::integral_constant<bool, true>{});
+  else
+    stream_loop(std::integral_constant<bool, false>{});
+  // ---- PV of the last tile (V buffer vb_prev) and the last item's rows
+  wait_vmem<0>();
+  __syncthreads();
+  {
+    const lds_u8* vb = lds + kVBuf + vb_prev * kTileBytes;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int db = 0; db < kDB; ++db) {
+          const lds_u8* p = vb + (kb * 32 + 16 * j) * 128 + (db >> 1) * C::kHalfBytes;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + voff[db & 1]));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + 8 * 128 + (voff[db & 1] ^ 16)));
+          O[db] = mfma32x32x16(concat(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi)), Pp[kb][j],
+                               O[db]);
+        }
+  }
+  epilogue(c_e, l_run);
+}
+
 // Name of a flash_fwd_kernel instantiation, as the profiler prints it.
 template <int MASK, int D, int WAVES>
 const char* flash_kernel_name() {
@@ -715,11 +1306,38 @@ int launch_one(const FlashArgs& a, hipStream_t stream, const char** launched) {
   return (int)hipGetLastError();
 }
 
-// The workgroup size (4 or 8 waves) comes from the launch plan in a.waves.
+template <int D>
+const char* flash_stream_kernel_name() {
+  static const std::string name = "flash_stream_kernel<" + std::to_string(D) + ">";
+  return name.c_str();
+}
+
+// The persistent kernel: one workgroup per CU, a multiple of 8 (the XCDs).
+// A workgroup's items start within 1/groups of the work (items with keys
+// weigh at least 2), so it holds at most work / (2 * groups) + 1 of them;
+// grids whose workgroups could exceed the LDS table run the 128-query
+// kernel instead.
+template <int D>
+int launch_stream(const FlashArgs& a, hipStream_t stream, const char** launched) {
+  const int groups = std::max(8, device_cu_count() / 8 * 8);
+  const int64_t n_qt = (a.Sq + 255) / 256;
+  const int64_t work = n_qt * a.H * a.B * ((a.Sk + kBN - 1) / kBN + 1);
+  if (work / (2 * groups) + 2 > kStreamTabMax) return launch_one<kMaskNone, 4, D>(a, stream, launched);
+  hipLaunchKernelGGL((flash_stream_kernel<D>), dim3(groups), dim3(512), 0, stream, a);
+  *launched = flash_stream_kernel_name<D>();
+  return (int)hipGetLastError();
+}
+
+// The workgroup size (4 or 8 waves) comes from the launch plan in a.waves,
+// and a.stream picks the persistent kernel for short key sequences.
 // (the per-(query, key) bias path, and key validity together with a key
 // bias, always run 128-query workgroups)
 template <int MASK>
 int launch(const FlashArgs& a, hipStream_t stream, const char** launched) {
+  if constexpr (MASK == kMaskNone) {
+    if (a.stream)
+      return a.D == 64 ? launch_stream<64>(a, stream, launched) : launch_stream<128>(a, stream, launched);
+  }
   constexpr bool kOnly4 = (MASK & kMaskFull) || MASK == (kMaskValid | kMaskBias);
   if (a.waves == 4 || kOnly4)
     return a.D == 64 ? launch_one<MASK, 4, 64>(a, stream, launched) : launch_one<MASK, 4, 128>(a, stream, launched);

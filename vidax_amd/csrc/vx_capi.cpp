@@ -73,9 +73,12 @@ struct FlashTileRule {
   const char* arch;
   int32_t max_seq_k_small;    // key sequences up to this run 128-query workgroups
   int64_t min_tiles_large;    // grids with fewer 256-query tiles run 128-query workgroups
+  // ... except grids of at least this many 256-query tiles with no key
+  // masks but kv_len, which run the persistent 256-query kernel
+  int64_t min_tiles_stream;
 };
 constexpr FlashTileRule kFlashTileTable[] = {
-    {"gfx950", 1024, 768},
+    {"gfx950", 1024, 768, 4096},
 };
 constexpr int32_t kKeyTile = 64;
 
@@ -138,25 +141,46 @@ const FlashTileOverride& tile_override() {
 // per-(query, key) bias (short text-encoder sequences) and key validity
 // together with a key bias (a rare pair, which needs more registers than
 // the 256-query kernel has without spilling) run 128-query workgroups.
-int32_t flash_plan(int32_t B, int32_t Sq, int32_t Sk, int32_t H, int32_t mask_kind, int32_t* waves) {
+//
+// stream (optional): set to 1 when the plan picks the persistent 256-query
+// kernel (key sequences up to max_seq_k_small, at least min_tiles_stream
+// 256-query tiles, no key masks but kv_len, at most 64 batch items, few
+// enough items per workgroup for its table). The override 128 turns it off;
+// 256 keeps the rule.
+int32_t flash_plan(int32_t B, int32_t Sq, int32_t Sk, int32_t H, int32_t mask_kind, int32_t* waves,
+                   int32_t* stream = nullptr) {
   const FlashTileOverride& o = tile_override();
   if (o.rc != VX_OK) return fail(o.rc, "%s", o.error.c_str());
+  if (stream != nullptr) *stream = 0;
   if ((mask_kind & 4) != 0 || (mask_kind & 3) == 3) {
     *waves = 4;
     return VX_OK;
   }
-  if (o.block_q != 0) {
-    *waves = o.block_q / 32;
-    return VX_OK;
-  }
   const FlashTileRule& r = kFlashTileTable[0];
   const int64_t tiles256 = (int64_t)((Sq + 255) / 256) * H * B;
+  const int64_t key_tiles = ((int64_t)Sk + kKeyTile - 1) / kKeyTile;
+  const bool streamable = mask_kind == 0 && Sk <= r.max_seq_k_small && tiles256 >= r.min_tiles_stream && B <= 64 &&
+                          tiles256 * (key_tiles + 1) / (2 * 256) + 2 <= vx::kStreamTabMax;
+  if (o.block_q != 0) {
+    *waves = o.block_q / 32;
+    if (stream != nullptr) *stream = *waves == 8 && streamable ? 1 : 0;
+    return VX_OK;
+  }
+  if (streamable) {
+    *waves = 8;
+    if (stream != nullptr) *stream = 1;
+    return VX_OK;
+  }
   *waves = (Sk <= r.max_seq_k_small || tiles256 < r.min_tiles_large) ? 4 : 8;
   return VX_OK;
 }
 
-void flash_kernel_label(int32_t mask_kind, int32_t D, int32_t waves, char* out, int32_t len) {
-  if (out != nullptr && len > 0) snprintf(out, (size_t)len, "flash_fwd_kernel<%d, %d, %d>", mask_kind, D, waves);
+void flash_kernel_label(int32_t mask_kind, int32_t D, int32_t waves, int32_t stream, char* out, int32_t len) {
+  if (out == nullptr || len <= 0) return;
+  if (stream)
+    snprintf(out, (size_t)len, "flash_stream_kernel<%d>", D);
+  else
+    snprintf(out, (size_t)len, "flash_fwd_kernel<%d, %d, %d>", mask_kind, D, waves);
 }
 
 // ---- key split of the last round of a grid (vx_flash_attn_ws_fwd).
@@ -269,12 +293,15 @@ int32_t flash_check(const void* q, const void* k, const void* v, const void* out
   if (ks[1] > (int64_t(1) << 24) || vs[1] > (int64_t(1) << 24))
     return fail(VX_ERR_UNSUPPORTED, "k/v sequence strides (%lld, %lld) above 2^24 elements are not supported",
                 (long long)ks[1], (long long)vs[1]);
-  int32_t waves = 0;
+  int32_t waves = 0, stream = 0;
   const int32_t mask_kind =
       (key_valid != nullptr ? 1 : 0) | (key_bias != nullptr ? 2 : 0) | (full_bias != nullptr ? 4 : 0);
-  if ((rc = flash_plan(B, Sq, Sk, H, mask_kind, &waves)) != VX_OK) return rc;
+  if ((rc = flash_plan(B, Sq, Sk, H, mask_kind, &waves, &stream)) != VX_OK) return rc;
+  // the persistent kernel copies q tiles with 32-bit row offsets too
+  if (qs[1] > (int64_t(1) << 24)) stream = 0;
   if (args != nullptr) {
     args->waves = waves;
+    args->stream = stream;
     args->split_items = 0;
     args->k_mid = 0;
     args->ws = nullptr;
@@ -478,10 +505,11 @@ int32_t vx_flash_attn_split_plan(int32_t batch, int32_t seq_q, int32_t seq_k, in
     return fail(VX_ERR_INVALID_ARGUMENT, "batch, seq_q, seq_k and num_heads must be >= 1");
   if (head_dim != 128 && head_dim != 64)
     return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 64 and 128)", head_dim);
-  int32_t waves = 0;
-  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, 0, &waves);
+  int32_t waves = 0, stream = 0;
+  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, 0, &waves, &stream);
   if (rc != VX_OK) return rc;
-  const SplitPlan p = flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, waves, num_cus);
+  const SplitPlan p =
+      stream ? SplitPlan{} : flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, waves, num_cus);
   if (split_items != nullptr) *split_items = p.items;
   if (split_key != nullptr) *split_key = p.k_mid;
   if (workspace_bytes != nullptr) *workspace_bytes = p.ws_bytes;
@@ -511,10 +539,11 @@ int32_t vx_flash_attn_ws_fwd(const void* q, const void* k, const void* v, void* 
   if (workspace != nullptr && !aligned16(workspace))
     return fail(VX_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   if ((rc = injected()) != VX_OK) return rc;
-  // (calls with a key bias are not split)
-  const SplitPlan p = key_bias != nullptr ? SplitPlan{}
-                                          : flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, args.waves,
-                                                             vx::device_cu_count());
+  // (calls with a key bias, and the persistent short-key kernel, are not split)
+  const SplitPlan p = key_bias != nullptr || args.stream
+                          ? SplitPlan{}
+                          : flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, args.waves,
+                                             vx::device_cu_count());
   if (p.items > 0 && workspace != nullptr && workspace_bytes >= p.ws_bytes) {
     args.split_items = p.items;
     args.k_mid = p.k_mid;
@@ -534,10 +563,10 @@ int32_t vx_flash_attn_plan(int32_t batch, int32_t seq_q, int32_t seq_k, int32_t 
   if (head_dim != 128 && head_dim != 64)
     return fail(VX_ERR_UNSUPPORTED, "head_dim %d is not supported (this build handles 64 and 128)", head_dim);
   if (mask_kind < 0 || mask_kind > 7) return fail(VX_ERR_INVALID_ARGUMENT, "mask_kind must be in 0..7");
-  int32_t waves = 0;
-  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, mask_kind, &waves);
+  int32_t waves = 0, stream = 0;
+  const int32_t rc = flash_plan(batch, seq_q, seq_k, num_heads, mask_kind, &waves, &stream);
   if (rc != VX_OK) return rc;
-  flash_kernel_label(mask_kind, head_dim, waves, kernel_name, name_len);
+  flash_kernel_label(mask_kind, head_dim, waves, stream, kernel_name, name_len);
   return ok();
 }
 
@@ -594,9 +623,10 @@ int32_t vx_flash_attn_noalloc_fwd(const void* q, const void* k, const void* v, v
                            num_heads, head_dim, q_strides, k_strides, v_strides, out_strides, scale, &args);
   if (rc != VX_OK) return rc;
   if ((rc = injected()) != VX_OK) return rc;
-  const SplitPlan p = key_bias != nullptr ? SplitPlan{}
-                                          : flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, args.waves,
-                                                             vx::device_cu_count());
+  const SplitPlan p = key_bias != nullptr || args.stream
+                          ? SplitPlan{}
+                          : flash_split_plan(batch, seq_q, seq_k, num_heads, head_dim, args.waves,
+                                             vx::device_cu_count());
   if (p.items > 0) {
     void* ws = nullptr;
     int64_t cap = 0;

@@ -24,6 +24,9 @@ struct FlashArgs {
   int64_t qs[3], ks[3], vs[3], os[3];
   float scale;  // softmax scale (> 0)
   int32_t waves;  // workgroup size chosen by the launch plan: 4 (128 queries) or 8 (256)
+  // 1: the persistent 256-query kernel for short key sequences (waves 8, no
+  // key masks but kv_len, no key split), chosen by the launch plan
+  int32_t stream;
   // Key split chosen by the launch plan (split_items = 0: none): each of the
   // last split_items (query tile, head, batch) items runs as two workgroups
   // over keys [0, k_mid) and [k_mid, Sk), writing fp32 partials to ws
@@ -32,6 +35,14 @@ struct FlashArgs {
   int32_t k_mid;
   float* ws;
 };
+
+// Items (with keys) one workgroup of the persistent short-key kernel holds
+// in its LDS table. A workgroup's items start within 1/groups of the work
+// (key tiles + 1 per item; items with keys weigh at least 2), so it holds at
+// most work / (2 * groups) + 1 of them: the plan picks the kernel only for
+// grids with work / (2 * 256) + 2 <= kStreamTabMax, and the launcher checks
+// the same with the device's workgroup count.
+constexpr int kStreamTabMax = 1024;
 
 // fp32 values of one key-split partial: the lanes' O accumulators, then
 // (reference point, row sum) per lane.
