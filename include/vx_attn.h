@@ -316,14 +316,21 @@ int32_t vx_rmsnorm_scale_rope_check(const void* x, const void* out, const float*
 /*
  * Launch plan of vx_flash_attn_fwd / vx_flash_attn_bias_fwd for a shape (host
  * only, no GPU): writes the name of the kernel those calls would launch,
- * "flash_fwd_kernel<mask_kind, head_dim, waves>", into kernel_name
- * (name_len bytes, NUL-terminated). mask_kind is a bit set: 1 key_valid,
- * 2 key_bias, 4 a per-(query, key) bias. waves is 8 (256-query workgroups)
- * for long key sequences on large grids, else 4 (128-query workgroups), per
- * the library's gfx950 tile table; the environment variable
+ * "flash_fwd_kernel<mask_kind, head_dim, waves>" or
+ * "flash_stream_kernel<head_dim>", into kernel_name (name_len bytes,
+ * NUL-terminated). mask_kind is a bit set: 1 key_valid, 2 key_bias, 4 a
+ * per-(query, key) bias. waves is 8 (256-query workgroups) for long key
+ * sequences on large grids, else 4 (128-query workgroups), per the
+ * library's gfx950 tile table; key sequences up to 1024 with no key masks
+ * but kv_len, at most 64 batch items and at least 4096 256-query tiles (up
+ * to about 500k tile-steps) run the persistent 256-query kernel
+ * flash_stream_kernel (one workgroup per CU; on a device with fewer than 256
+ * CUs a grid too large for its item table runs the 4-wave kernel instead).
+ * The environment variable
  * VIDAX_FLASH_BLOCK_SIZES="block_q,block_k_major,block_k" (block_q 128 or
- * 256, key tiles 64) or "default" overrides it. A per-(query, key) bias, or
- * key_valid together with key_bias, always runs 4 waves. The variable is read once,
+ * 256, key tiles 64) or "default" overrides the workgroup size (128 turns the
+ * persistent kernel off). A per-(query, key) bias, or key_valid together
+ * with key_bias, always runs 4 waves. The variable is read once,
  * at the first flash call or plan of the process; a malformed value makes
  * every flash call and plan fail with VX_ERR_INVALID_ARGUMENT, an
  * unsupported one with VX_ERR_UNSUPPORTED.
