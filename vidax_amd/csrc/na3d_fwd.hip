@@ -115,8 +115,12 @@ __device__ __forceinline__ void prep_q(bf16x8 (&qr)[NDS], int hf, int64_t tok, c
   }
 }
 
+// Two waves per SIMD (256 registers a wave): its waves stream K from global
+// memory, so the second wave covers those loads' latency (at D = 128 the
+// kernel had 346 registers and one wave per SIMD: 1.9x slower at a (3,7,31)
+// window); the allocator spills one 8-byte value outside the key loop.
 template <int D>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
   constexpr int kRB = D * 2;              // bytes of one key
   constexpr int kCB = kChunk * kRB;       // one chunk of V in LDS
