@@ -805,10 +805,10 @@ void flash_stream_kernel(const FlashArgs a) {
   // ---- LDS offsets (the layout of flash_tile: half-planes of 64 rows x
   // 128 bytes, 16-byte chunks XOR-swizzled per row)
   // K fragment (kb, ds): key kb*32 + col, chunk 2*(ds%4) + hf of half ds/4,
-  // at koff0 ^ ((ds % 4) << 5) (2*(ds%4) + hf = 2*(ds%4) ^ hf). Inside the
-  // key loop the offsets (and the V ones derived from voff) are formed at
-  // each use from values made opaque by an empty asm, so that they do not
-  // hold registers across the whole loop, which has none to spare.
+  // at koff0 ^ ((ds % 4) << 5) (2*(ds%4) + hf = 2*(ds%4) ^ hf). The q
+  // reloads inside the key loop form their offsets at each use from a value
+  // made opaque by an empty asm, so that those do not hold registers across
+  // the whole loop, which has none to spare.
   const int koff0 = col * 128 + ((hf ^ half_swizzle(col)) * 16);
   auto kofs = [&](int d4) { return koff0 ^ (d4 << 5); };
   auto kofs_loop = [&](int d4) {
@@ -824,23 +824,7 @@ void flash_stream_kernel(const FlashArgs a) {
     const int key = hf * 4 + vr;
     voff[db1] = key * 128 + (((4 * db1 + 2 * dh + (vc4 >> 1)) ^ half_swizzle(key)) * 16) + (vc4 & 1) * 8;
   }
-  const int srow = lane >> 3, scol = lane & 7;
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
-  struct Lanes {
-    uint32_t k[kLoadsPerWave], v[kLoadsPerWave];
-  };
-  auto make_lanes = [&]() {
-    Lanes ln;
-#pragma unroll
-    for (int p = 0; p < kLoadsPerWave; ++p) {
-      const int i = (wave % kCopyWaves) * kLoadsPerWave + p;
-      const int r = 8 * (i & 7) + srow;
-      const int col_el = (i >> 3) * 64 + ((scol ^ half_swizzle(r)) * 8);
-      ln.k[p] = (uint32_t)(r * (int)a.ks[1] + col_el) * 2u;
-      ln.v[p] = (uint32_t)(r * (int)a.vs[1] + col_el) * 2u;
-    }
-    return ln;
-  };
   const uint64_t q_addr = uniform_u64((uint64_t)(uintptr_t)a.q);
   const uint64_t k_addr = uniform_u64((uint64_t)(uintptr_t)a.k);
   const uint64_t v_addr = uniform_u64((uint64_t)(uintptr_t)a.v);
@@ -848,7 +832,7 @@ void flash_stream_kernel(const FlashArgs a) {
   const uint64_t v_tile_bytes = uniform_u64((uint64_t)a.vs[1] * (2 * kBN));
   // this wave's copies of 64 rows from byte address `addr` into the LDS tile
   // at buf_off; rows from rows_left on repeat row rows_left - 1 (>= 0)
-  // (the per-lane terms are formed at each call: an empty asm on the lane
+  // (the per-lane offsets are formed at each call: an empty asm on the lane
   // index keeps them out of the registers of the whole key loop)
   auto stage_clamped = [&](uint64_t addr, int64_t stride, int rows_left, int buf_off) {
     const i32x4_rsrc rs = raw_rsrc_u64(addr);
@@ -863,17 +847,6 @@ void flash_stream_kernel(const FlashArgs a) {
       const int rr = min(r, rows_left - 1);
       const uint32_t off = (uint32_t)(rr * (int)stride + (i >> 3) * 64 + ((sc ^ half_swizzle(r)) * 8)) * 2u;
       lds_dma16_buf(rs, off, dst + p * 1024);
-    }
-  };
-  auto stage_rows = [&](uint64_t addr, const uint32_t (&lanep)[kLoadsPerWave], int64_t stride, int rows_left,
-                        int buf_off) {
-    if (rows_left >= kBN) {
-      const i32x4_rsrc rs = raw_rsrc_u64(addr);
-      const uint32_t dst = lds_base + buf_off + (uint32_t)(wave * kLoadsPerWave) * 1024u;
-#pragma unroll
-      for (int p = 0; p < kLoadsPerWave; ++p) lds_dma16_buf(rs, lanep[p], dst + p * 1024);
-    } else {
-      stage_clamped(addr, stride, rows_left, buf_off);
     }
   };
   // q rows of table entry e (4 x 64 rows; rows past Sq repeat row Sq - 1)
@@ -975,13 +948,12 @@ void flash_stream_kernel(const FlashArgs a) {
   CopyCur kc{}, vc{};
   bf16x8 qr[kDS];
   if (wave < kCopyWaves) {
-    const Lanes ln = make_lanes();
     open_copy(kc, 0, k_addr, a.ks);
     open_copy(vc, 0, v_addr, a.vs);
     stage_q(0);
 #pragma unroll
     for (int j = 0; j < kKNB; ++j) {
-      stage_rows(kc.addr, ln.k, a.ks[1], kc.rows, kKBuf + j * kTileBytes);
+      stage_clamped(kc.addr, a.ks[1], kc.rows, kKBuf + j * kTileBytes);
       advance_copy(kc, k_addr, a.ks, k_tile_bytes);
     }
   }
@@ -1025,7 +997,7 @@ void flash_stream_kernel(const FlashArgs a) {
   // steps, below): consumes S (scores of tile u) and Pp (probabilities of
   // tile u-1), produces Sn (scores of tile u+1) and P (probabilities of tile
   // u); returns the row sum of P (this lane's part).
-  auto step = [&](auto copy_tag, const Lanes& ln, const int u, f32x16 (&S)[2], f32x16 (&Sn)[2],
+  auto step = [&](auto copy_tag, const int u, f32x16 (&S)[2], f32x16 (&Sn)[2],
                   const bf16x8 (&Pp)[2][2], bf16x8 (&P)[2][2]) __attribute__((always_inline)) -> float {
     constexpr bool COPY = decltype(copy_tag)::value;
     const bool first = c_t == 0;
@@ -1038,9 +1010,9 @@ void flash_stream_kernel(const FlashArgs a) {
       // the next item's q (items of two or more tiles) first: the waits
       // count the tile copies after it
       if (first && c_n > 1 && u + c_n < U) stage_q(c_e + 1);
-      stage_rows(vc.addr, ln.v, a.vs[1], vc.rows, kVBuf + (vb_prev ^ 1) * kTileBytes);
+      stage_clamped(vc.addr, a.vs[1], vc.rows, kVBuf + (vb_prev ^ 1) * kTileBytes);
       advance_copy(vc, v_addr, a.vs, v_tile_bytes);
-      stage_rows(kc.addr, ln.k, a.ks[1], kc.rows, kKBuf + kb_next * kTileBytes);
+      stage_clamped(kc.addr, a.ks[1], kc.rows, kKBuf + kb_next * kTileBytes);
       advance_copy(kc, k_addr, a.ks, k_tile_bytes);
     }
     float cc_ = c;
@@ -1071,14 +1043,13 @@ void flash_stream_kernel(const FlashArgs a) {
         if (s < kPV) {
           const int db = s % kDB, j = (s / kDB) & 1, kb = s / (2 * kDB);
           const lds_u8* p = vb0 + (kb * 32 + 16 * j) * 128 + (db >> 1) * C::kHalfBytes;
-          int vo = voff[db & 1];
-          asm volatile("" : "+v"(vo));
+          const int vo = voff[db & 1];
           const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + vo));
           const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p + 8 * 128 + (vo ^ 16)));
           return concat(__builtin_bit_cast(bf16x4, lo), __builtin_bit_cast(bf16x4, hi));
         }
         const int ds = (s - kPV) >> 1, kb = (s - kPV) & 1;
-        return *(const VX_LDS bf16x8*)(kb0 + kofs_loop(ds & 3) + kb * 32 * 128 + (ds >> 2) * C::kHalfBytes);
+        return *(const VX_LDS bf16x8*)(kb0 + kofs(ds & 3) + kb * 32 * 128 + (ds >> 2) * C::kHalfBytes);
       };
       const bf16x2 one2 = {(bf16)1.0f, (bf16)1.0f};
       if (!COPY) __builtin_amdgcn_s_setprio(1);
@@ -1184,7 +1155,7 @@ void flash_stream_kernel(const FlashArgs a) {
   // first: its own QK^T slots score that item); after it, the previous
   // item's rows are stored and O restarts; after the step that scored the
   // item's last tile, the next item's q is loaded for the next step's slots.
-  auto stream_step = [&](auto copy_tag, const Lanes& ln, const int u, f32x16 (&S)[2], f32x16 (&Sn)[2],
+  auto stream_step = [&](auto copy_tag, const int u, f32x16 (&S)[2], f32x16 (&Sn)[2],
                          const bf16x8 (&Pp)[2][2], bf16x8 (&P)[2][2]) __attribute__((always_inline)) {
     constexpr bool COPY = decltype(copy_tag)::value;
     const bool first = c_t == 0, last = c_t + 1 == c_n;
@@ -1198,7 +1169,7 @@ void flash_stream_kernel(const FlashArgs a) {
         load_q(qr);
       }
     }
-    const float l_tile = step(copy_tag, ln, u, S, Sn, Pp, P);
+    const float l_tile = step(copy_tag, u, S, Sn, Pp, P);
     stored = first && has_prev;
     if (first) {
       if (has_prev) epilogue(c_e - 1, l_run);
@@ -1230,15 +1201,13 @@ void flash_stream_kernel(const FlashArgs a) {
   f32x16 S2[2];
   bf16x8 P2[2][2];
   auto stream_loop = [&](auto copy_tag) __attribute__((always_inline)) {
-    Lanes ln{};
-    if constexpr (decltype(copy_tag)::value) ln = make_lanes();
     int u = 0;
     for (; u + 1 < U; u += 2) {
-      stream_step(copy_tag, ln, u, S, S2, Pp, P2);
-      stream_step(copy_tag, ln, u + 1, S2, S, P2, Pp);
+      stream_step(copy_tag, u, S, S2, Pp, P2);
+      stream_step(copy_tag, u + 1, S2, S, P2, Pp);
     }
     if (u < U) {
-      stream_step(copy_tag, ln, u, S, S2, Pp, P2);
+      stream_step(copy_tag, u, S, S2, Pp, P2);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
