@@ -725,7 +725,7 @@ void flash_stream_kernel(const FlashArgs a) {
   const int n_qt = (a.Sq + 255) / 256;
   const int per_b = a.H * n_qt;  // items per batch item
   auto uni = [](int x) { return __builtin_amdgcn_readfirstlane(x); };
-  auto kv_end_of = [&](int b) -> int {
+  auto kv_end_of = [&](int b) __attribute__((always_inline)) -> int {
     int kv = a.Sk;
     if (a.kv_len != nullptr) kv = min(max(a.kv_len[b], 0), a.Sk);
     return uni(kv);
@@ -738,7 +738,7 @@ void flash_stream_kernel(const FlashArgs a) {
   for (int b = 0; b < a.B; ++b) W += (int64_t)per_b * (tiles_of(kv_end_of(b)) + 1);
   const int G = gridDim.x;
   const int chunk_id = (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8;
-  auto first_item_at = [&](int64_t x) -> int {  // first item starting at or after work x
+  auto first_item_at = [&](int64_t x) __attribute__((always_inline)) -> int {  // first item starting at or after work x
     int64_t P = 0;
     for (int b = 0; b < a.B; ++b) {
       const int w = tiles_of(kv_end_of(b)) + 1;
@@ -797,7 +797,7 @@ void flash_stream_kernel(const FlashArgs a) {
   struct Item {
     int b, h, qt, kv;
   };
-  auto entry = [&](int e) -> Item {
+  auto entry = [&](int e) __attribute__((always_inline)) -> Item {
     const i32x4 v = *(const VX_LDS i32x4*)(lds + kTab + e * 16);
     return Item{uni(v[0]), uni(v[1]), uni(v[2]), uni(v[3])};
   };
@@ -811,7 +811,7 @@ void flash_stream_kernel(const FlashArgs a) {
   // the whole loop, which has none to spare.
   const int koff0 = col * 128 + ((hf ^ half_swizzle(col)) * 16);
   auto kofs = [&](int d4) { return koff0 ^ (d4 << 5); };
-  auto kofs_loop = [&](int d4) {
+  auto kofs_loop = [&](int d4) __attribute__((always_inline)) {
     int k = koff0;
     asm volatile("" : "+v"(k));
     return k ^ (d4 << 5);
@@ -834,12 +834,25 @@ void flash_stream_kernel(const FlashArgs a) {
   // at buf_off; rows from rows_left on repeat row rows_left - 1 (>= 0)
   // (the per-lane offsets are formed at each call: an empty asm on the lane
   // index keeps them out of the registers of the whole key loop)
-  auto stage_clamped = [&](uint64_t addr, int64_t stride, int rows_left, int buf_off) {
+  auto stage_clamped = [&](uint64_t addr, int64_t stride, int rows_left, int buf_off) __attribute__((always_inline)) {
     const i32x4_rsrc rs = raw_rsrc_u64(addr);
     const uint32_t dst = lds_base + buf_off + (uint32_t)(wave * kLoadsPerWave) * 1024u;
     int ln_ = lane;
     asm volatile("" : "+v"(ln_));
     const int sr = ln_ >> 3, sc = ln_ & 7;
+    if (rows_left >= kBN) {
+      // row r = 8*(i%8) + sr: its swizzle depends on sr and on bit 0 of i,
+      // the rest of the offset is uniform
+      const uint32_t lane0 = (uint32_t)(sr * (int)stride + ((sc ^ half_swizzle(sr)) * 8)) * 2u;
+      const uint32_t lane1 = (uint32_t)(sr * (int)stride + ((sc ^ half_swizzle(sr + 8)) * 8)) * 2u;
+#pragma unroll
+      for (int p = 0; p < kLoadsPerWave; ++p) {
+        const int i = wave * kLoadsPerWave + p;
+        const uint32_t row0 = (uint32_t)(8 * (i & 7) * (int)stride + (i >> 3) * 64) * 2u;
+        lds_dma16_buf(rs, ((i & 1) ? lane1 : lane0) + row0, dst + p * 1024);
+      }
+      return;
+    }
 #pragma unroll
     for (int p = 0; p < kLoadsPerWave; ++p) {
       const int i = wave * kLoadsPerWave + p;
@@ -850,7 +863,7 @@ void flash_stream_kernel(const FlashArgs a) {
     }
   };
   // q rows of table entry e (4 x 64 rows; rows past Sq repeat row Sq - 1)
-  auto stage_q = [&](int e) {
+  auto stage_q = [&](int e) __attribute__((always_inline)) {
     const Item it = entry(e);
     const uint64_t head = q_addr + (uint64_t)((int64_t)it.b * a.qs[0] + (int64_t)it.h * a.qs[2]) * 2u;
 #pragma unroll
@@ -860,7 +873,7 @@ void flash_stream_kernel(const FlashArgs a) {
     }
   };
   // this wave's 32 q rows from the q buffer (the B operand of QK^T)
-  auto load_q = [&](bf16x8 (&qr)[kDS]) {
+  auto load_q = [&](bf16x8 (&qr)[kDS]) __attribute__((always_inline)) {
     const lds_u8* qb = lds + kQBuf + (wave >> 1) * kTileBytes + (wave & 1) * 32 * 128;
 #pragma unroll
     for (int ds = 0; ds < kDS; ++ds)
@@ -875,14 +888,14 @@ void flash_stream_kernel(const FlashArgs a) {
     uint64_t addr;
     int rows, left, e;
   };
-  auto open_copy = [&](CopyCur& c, int e, uint64_t base, const int64_t (&s)[3]) {
+  auto open_copy = [&](CopyCur& c, int e, uint64_t base, const int64_t (&s)[3]) __attribute__((always_inline)) {
     const Item it = entry(e);
     c.e = e;
     c.rows = it.kv;
     c.left = tiles_of(it.kv);
     c.addr = uniform_u64(base + (uint64_t)((int64_t)it.b * s[0] + (int64_t)it.h * s[2]) * 2u);
   };
-  auto advance_copy = [&](CopyCur& c, uint64_t base, const int64_t (&s)[3], uint64_t tile_bytes) {
+  auto advance_copy = [&](CopyCur& c, uint64_t base, const int64_t (&s)[3], uint64_t tile_bytes) __attribute__((always_inline)) {
     if (c.left > 1) {
       --c.left;
       c.rows -= kBN;
@@ -910,7 +923,7 @@ void flash_stream_kernel(const FlashArgs a) {
   // Lanes past Sq hold row Sq-1's query (the q copies repeat that row), so
   // they store row Sq-1's output again, the same bytes: every wave issues
   // exactly 2 * kDB stores, which the copying waves' waits count.
-  auto epilogue = [&](int e, float l) {
+  auto epilogue = [&](int e, float l) __attribute__((always_inline)) {
     const float lt = halves_sum(l);
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     const Item it = entry(e);
@@ -927,7 +940,7 @@ void flash_stream_kernel(const FlashArgs a) {
       for (int pr = 0; pr < 2; ++pr) *(u32x4*)(orow + db * 32 + (2 * pr + (ln_ >> 5)) * 8) = chunk[0][pr];
     }
   };
-  auto probs = [&](const f32x16 (&S)[2], float cc_, float m, bf16x8 (&P)[2][2]) -> float {
+  auto probs = [&](const f32x16 (&S)[2], float cc_, float m, bf16x8 (&P)[2][2]) __attribute__((always_inline)) -> float {
     const float mneg = -m;
     float l = 0.f;
 #pragma unroll
@@ -966,7 +979,7 @@ void flash_stream_kernel(const FlashArgs a) {
   // (`stored`: the previous step ended an item). Only the copying waves
   // wait; the barrier after the wait publishes their copies to all waves.
   bool stored = false;
-  auto wait_prev = [&]() {
+  auto wait_prev = [&]() __attribute__((always_inline)) {
     if (wave < kCopyWaves) {
       if (stored)
         wait_vmem<kLoadsPerWave + 2 * kDB>();
@@ -1039,7 +1052,7 @@ void flash_stream_kernel(const FlashArgs a) {
     {
       const lds_u8* kb0 = lds + kKBuf + kb_cur * kTileBytes;
       const lds_u8* vb0 = lds + kVBuf + vb_prev * kTileBytes;
-      auto frag = [&](int s) -> bf16x8 {
+      auto frag = [&](int s) __attribute__((always_inline)) -> bf16x8 {
         if (s < kPV) {
           const int db = s % kDB, j = (s / kDB) & 1, kb = s / (2 * kDB);
           const lds_u8* p = vb0 + (kb * 32 + 16 * j) * 128 + (db >> 1) * C::kHalfBytes;
@@ -1059,7 +1072,7 @@ void flash_stream_kernel(const FlashArgs a) {
       fr[0] = frag(0);
       fr[1] = frag(1);
       fr[2] = frag(2);
-      auto softmax_block = [&]() {
+      auto softmax_block = [&]() __attribute__((always_inline)) {
         const float mneg = -m_run;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -1077,7 +1090,7 @@ void flash_stream_kernel(const FlashArgs a) {
         for (int i = 0; i < 16; ++i) l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[i], one2, l_tile, false);
         __builtin_amdgcn_sched_barrier(0);
       };
-      auto pack_p = [&]() {
+      auto pack_p = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -1093,7 +1106,7 @@ void flash_stream_kernel(const FlashArgs a) {
       // it before their slots (the scores are then dead during the slots,
       // which keeps the kernel within its registers) and rescale O after
       // them; the results are the same.
-      auto rare_path = [&]() {
+      auto rare_path = [&]() __attribute__((always_inline)) {
         if (__builtin_amdgcn_ballot_w64(l_tile > kSumLimit || is_nan_bits(l_tile)) != 0) {
           rare = true;
           float mxc = -__builtin_inff();
@@ -1112,7 +1125,7 @@ void flash_stream_kernel(const FlashArgs a) {
       };
       // an item's first tile takes its max first (m_run = the rare path's
       // reference point for it), so that the speculative pass stands
-      auto tile_probs = [&]() {
+      auto tile_probs = [&]() __attribute__((always_inline)) {
         if (first) {
           float mxc = -__builtin_inff();
 #pragma unroll
