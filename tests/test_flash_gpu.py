@@ -572,6 +572,7 @@ STREAM_CASES = [
     (2, 20000, 130, 26, 128, [1, 64], 162),      # one-tile items
     (1, 65536, 1024, 16, 128, None, 163),        # sixteen tiles, no kv_len
     (2, 32760, 512, 16, 64, [512, 20], 164),     # head dim 64
+    (2, 16384, 256, 32, 128, [0, 0], 166),       # no keys at all: zero rows only
 ]
 
 
