@@ -824,8 +824,13 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   }
 }
 
+// Three waves per SIMD for the 32-key segments at head dim 64 (146 VGPRs,
+// three 32 KiB workgroups per CU): 33x88x160 NH=4 at a (5,5,21) window
+// 1.02 -> 0.94 ms. The 16-key form gained at 21x45x80 NH=24 (-9 %) but lost
+// at 33x88x160 NH=4 (+3.5 %) and keeps two.
 template <int SEG, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 && SEG == 32 ? 3 : 2,
+                                                                       D == 64 && SEG == 32 ? 3 : 2)))
 void na3d_pipe_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   na3d_pipe_body<SEG, D, false>(a, n_yb, n_xb);
 }
