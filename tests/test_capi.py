@@ -297,6 +297,12 @@ def test_na3d_kernel_name_follows_the_launch_rule():
     from vidax_amd.natten import na3d_kernel_name
     assert na3d_kernel_name(80, 7) == "na3d_pipe_kernel<16, 128>"
     assert na3d_kernel_name(80, 9, 64) == "na3d_pipe_kernel<16, 64>"
+    # head dim 64, kw' <= 9: the tall bricks unless they pad the y-x plane more
+    assert na3d_kernel_name(80, 7, 64, height=45) == "na3d_tall_kernel<64>"    # 48x80 vs 48x96
+    assert na3d_kernel_name(80, 5, 64, height=44) == "na3d_tall_kernel<64>"    # 48x80 vs 44x96
+    assert na3d_kernel_name(40, 7, 64, height=22) == "na3d_tall_kernel<64>"    # 24x48 vs 24x64
+    assert na3d_kernel_name(20, 7, 64, height=11) == "na3d_pipe_kernel<16, 64>"  # 16x32 vs 12x32
+    assert na3d_kernel_name(80, 7, 128, height=45) == "na3d_pipe_kernel<16, 128>"
     assert na3d_kernel_name(80, 11, 64) == "na3d_tall_kernel<64>"        # 80 = 5 x 16, 96 in 32-wide bricks
     assert na3d_kernel_name(160, 11, 64) == "na3d_tall_wide_kernel<64>"  # 160 = 5 x 32
     assert na3d_kernel_name(104, 11, 64) == "na3d_tall_kernel<64>"       # 112 vs 128 columns

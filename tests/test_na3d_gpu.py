@@ -55,11 +55,15 @@ NA_CASES = [
 ]
 
 
-def _expected_kernel(W, kw, D):
+def _expected_kernel(H, W, kw, D):
     """The NA kernel for a clamped x window kw' = min(kw, W), written out
     here independently of the library's plan."""
     k = min(kw, W)
     if k <= 9:
+        # head dim 64: 1 x 8 x 16 bricks unless they cover more of the y-x
+        # plane than the 1 x 4 x 32 ones
+        if D == 64 and -(-H // 8) * 8 * (-(-W // 16) * 16) <= -(-H // 4) * 4 * (-(-W // 32) * 32):
+            return "na3d_tall_kernel<64>"
         return f"na3d_pipe_kernel<16, {D}>"
     if k <= 13:
         # head dim 64: 32-wide bricks unless they leave more ragged columns
@@ -77,7 +81,7 @@ def _run(gpu, shape, ks, seed, D):
     q, k, v = O.make_na3d_inputs(B, T, H, W, NH, D, seed)
     out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), ks)
     launched = _lib.last_launch()
-    assert launched == _expected_kernel(W, ks[2], D), launched
+    assert launched == _expected_kernel(H, W, ks[2], D), launched
     torch.cuda.synchronize()
     _check(out.float().cpu().numpy(), O.na3d(q, k, v, ks), f"oracle ({launched})")
 
@@ -99,6 +103,10 @@ NA_D64_CASES = [
     ((1, 3, 12, 40, 2), (3, 9, 9), 56),       # empty waves at the ragged x edge
     ((1, 5, 19, 64, 2), (5, 11, 11), 57),     # 32-wide tall bricks, two along x, ragged y
     ((2, 4, 10, 56, 1), (3, 13, 12), 58),     # 32-wide tall bricks, even window, two empty waves at x
+    ((1, 5, 11, 20, 2), (3, 7, 7), 59),       # stage-1 grid: 16-key segments (tall bricks would pad 11 rows to 16)
+    ((1, 3, 4, 64, 1), (3, 3, 5), 65),        # 16-key segments, one y brick
+    ((1, 4, 22, 40, 2), (3, 7, 7), 66),       # tall bricks at kw' = 7, ragged x (40 % 16)
+    ((2, 3, 13, 21, 1), (3, 5, 9), 67),       # tall bricks at kw' = 9, ragged y and x, even area
 ]
 
 
@@ -147,15 +155,16 @@ def test_na3d_wide_windows(gpu, shape, ks, seed, D):
 
 
 @pytest.mark.parametrize("shift", [-1000.0, -120.0, 200.0, 1000.0])
-@pytest.mark.parametrize("D", [128, 64])
-def test_na3d_row_offsets(gpu, shift, D):
+@pytest.mark.parametrize("D,H,W", [(128, 9, 20), (64, 9, 20), (64, 16, 16)])
+def test_na3d_row_offsets(gpu, shift, D, H, W):
     """A constant added to every score of a query leaves its softmax
     unchanged: key dim 0 all ones, the query's dim 0 = `shift` on every other
     x position (0 elsewhere), so queries far below 2^-100 or far above 2^8
-    (log2 units) sit next to ordinary ones in the same wave."""
-    from vidax_amd import neighborhood_attention_3d
-    _say(f"na3d row offsets shift={shift} D={D}")
-    B, T, H, W, NH = 1, 3, 9, 20, 2
+    (log2 units) sit next to ordinary ones in the same wave. The 16 x 16
+    grid runs the tall bricks at head dim 64."""
+    from vidax_amd import _lib, neighborhood_attention_3d
+    _say(f"na3d row offsets shift={shift} D={D} grid 3x{H}x{W}")
+    B, T, NH = 1, 3, 2
     rng = np.random.default_rng(71)
     q = O.bf16_round((0.3 * rng.standard_normal((B, T, H, W, NH, D))).astype(np.float32))
     k = O.bf16_round((0.3 * rng.standard_normal((B, T, H, W, NH, D))).astype(np.float32))
@@ -164,6 +173,7 @@ def test_na3d_row_offsets(gpu, shift, D):
     q[:, :, :, ::2, :, 0] = shift
     q[:, :, :, 1::2, :, 0] = 0.0
     out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), (3, 7, 7))
+    assert _lib.last_launch() == _expected_kernel(H, W, 7, D), _lib.last_launch()
     torch.cuda.synchronize()
     _check(out.float().cpu().numpy(), O.na3d(q, k, v, (3, 7, 7)), "oracle")
 

@@ -2,7 +2,8 @@
 // boundary-clamped windows), bf16 in/out, head dim 128 or 64.
 //
 // Three kernels, chosen by the clamped x window kw' (the launch plan of the
-// C ABI, Na3dVariant):
+// C ABI, Na3dVariant; at head dim 64 also by how the grid's y x x plane
+// rounds up to each brick shape):
 // - na3d_pipe_kernel<SEG, D> (kw' <= 9 or 13 < kw' <= 25): a workgroup of 4
 //   waves owns a 1 (t) x 4 (y) x 32 (x) query brick of one head and streams
 //   the union of its windows, kt' x NY key rows (t', y'), through LDS with
@@ -10,11 +11,12 @@
 //   queries need, 32 keys per step, and runs the flash kernel's software
 //   pipeline (QK^T of the next chunk and PV of the previous one interleaved
 //   with the masking and lazy-rescale softmax of the current one).
-// - na3d_tall_kernel<D> (9 < kw' <= 13): the same body on 1 x 8 x 16 bricks
+// - na3d_tall_kernel<D> (9 < kw' <= 13, and kw' <= 9 at head dim 64 when
+//   its bricks pad the grid no more): the same body on 1 x 8 x 16 bricks
 //   with waves of 8 y x 4 x queries, so that a wave's x window still fits a
 //   16-key segment; na3d_tall_wide_kernel<64> runs 1 x 8 x 32 bricks of 8
 //   such waves at head dim 64.
-// - na3d_wave_kernel (25 < kw' <= 57, D = 128): each wave owns a
+// - na3d_wave_kernel<D> (kw' > 25, any size, D 128 or 64): each wave owns a
 //   1 x 4 x 8 brick on its own and walks its (kt', ny, nx) key box in chunks
 //   of 32 keys, laid out as (t', y') rows of SEG = round_up(nx, 16)
 //   x-positions, with K fragments loaded straight from global memory and V

@@ -219,8 +219,18 @@ SplitPlan flash_split_plan(int32_t B, int32_t Sq, int32_t Sk, int32_t H, int32_t
 // ---- neighbourhood-attention launch plan, by the clamped x window (and for
 // head dim 64 with the tall bricks, the grid width: the 32-wide bricks when
 // they leave no more ragged columns than the 16-wide ones).
-int32_t na3d_variant(int32_t kw_clamped, int32_t D, int32_t W) {
-  if (kw_clamped <= 9) return vx::kNaPipe16;
+//
+// Head dim 64 with kw' <= 9 runs the tall 1 x 8 x 16 bricks (four waves per
+// SIMD) unless they pad the y-x plane more than the 1 x 4 x 32 bricks do
+// (same box, (3,7,7) and (3,5,5) windows: 5x22x40 NH=16 -10 %, 9x22x40 NH=8
+// -6 %, 21x45x80 NH=24 -5 %, 17x44x80 NH=8 even; 5x11x20 NH=32, where the
+// tall bricks cover 16 rows for 11, +37 %).
+int32_t na3d_variant(int32_t kw_clamped, int32_t D, int32_t Hs, int32_t W) {
+  if (kw_clamped <= 9) {
+    const int64_t tall_area = (int64_t)((Hs + 7) / 8 * 8) * ((W + 15) / 16 * 16);
+    const int64_t pipe_area = (int64_t)((Hs + 3) / 4 * 4) * ((W + 31) / 32 * 32);
+    return D == 64 && tall_area <= pipe_area ? vx::kNaTall : vx::kNaPipe16;
+  }
   if (kw_clamped <= 13) return D == 64 && (W + 31) / 32 * 32 == (W + 15) / 16 * 16 ? vx::kNaTallWide : vx::kNaTall;
   if (kw_clamped <= 25) return vx::kNaPipe32;
   return vx::kNaWave;
@@ -372,7 +382,7 @@ int32_t na3d_check(const void* q, const void* k, const void* v, const void* out,
     args->kh = kh < Hs ? kh : Hs;
     args->kw = kw < W ? kw : W;
     args->scale = scale;
-    args->variant = na3d_variant(args->kw, D, W);
+    args->variant = na3d_variant(args->kw, D, Hs, W);
     args->q_prep = 0;
     args->q_weight = nullptr;
     args->q_cos = args->q_sin = nullptr;
@@ -580,7 +590,7 @@ int32_t vx_na3d_plan(int32_t t, int32_t h, int32_t w, int32_t head_dim, int32_t 
   if (rc != VX_OK) return rc;
   const int32_t kw = kernel_w < w ? kernel_w : w;
   if (kernel_name != nullptr && name_len > 0)
-    snprintf(kernel_name, (size_t)name_len, "%s", na3d_kernel_label(na3d_variant(kw, head_dim, w), head_dim));
+    snprintf(kernel_name, (size_t)name_len, "%s", na3d_kernel_label(na3d_variant(kw, head_dim, h, w), head_dim));
   return ok();
 }
 
