@@ -454,18 +454,22 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   // from (the first one's accumulator input), so the x window costs no
   // instruction per score. Otherwise (the tall bricks at head dim 64, whose
   // short steps need four waves per SIMD, i.e. at most 128 VGPRs, which the
-  // extra accumulator input does not leave) +inf / -inf limits applied with
-  // one v_min3 per score together with the row's y/t limit, and row sums of
-  // the bf16 probabilities.
+  // extra accumulator input does not leave) a 0 / 0xffff mask per bf16 half
+  // of each packed probability pair, one v_and_b32 per two scores after the
+  // exponent (an out-of-window score may give +inf there, which the mask
+  // clears before the row sum), and row sums of the bf16 probabilities.
   constexpr bool kAccMask = !(TALL && D == 64);
   f32x16 xbias;
-  float xlim[16];
+  uint32_t xpk[8];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int p = (SEG == 16 ? ((i >> 2) & 1) * 8 : (i >> 2) * 8) + hf * 4 + (i & 3);
     const bool in = (unsigned)(p - sx) < (unsigned)kw;
     xbias[i] = in ? 0.0f : -__builtin_inff();
-    xlim[i] = in ? __builtin_inff() : -__builtin_inff();
+    if (i & 1)
+      xpk[i >> 1] |= in ? 0xffff0000u : 0u;
+    else
+      xpk[i >> 1] = in ? 0xffffu : 0u;
   }
   const f32x16 s_init = kAccMask ? xbias : f32x16{};
 
@@ -665,8 +669,6 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     // exponent offset per key row: -m_run, or -inf for a row outside the y
     // window (exp2 then gives 0)
     const float mrow[2] = {row_ok[0] ? -m_run : -__builtin_inff(), row_ok[1] ? -m_run : -__builtin_inff()};
-    const float rlim[2] = {row_ok[0] ? __builtin_inff() : -__builtin_inff(),
-                           row_ok[1] ? __builtin_inff() : -__builtin_inff()};
     const bf16x2 one2 = {(bf16)1.0f, (bf16)1.0f};
     float l_tile = 0.f;
     bf16x8 fr[C::kSlots];
@@ -698,17 +700,17 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          // (the tall D = 64 block: kAccMask is false)
-          S[8 * g + i] = __builtin_fminf(__builtin_fminf(S[8 * g + i], xlim[8 * g + i]), rlim[g]);
-          pf[8 * g + i] = __builtin_fmaf(S[8 * g + i], c2, -m_run);
-        }
+        for (int i = 0; i < 8; ++i) pf[8 * g + i] = __builtin_fmaf(S[8 * g + i], c2, mrow[g]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < 8; ++i) pf[8 * g + i] = fast_exp2(pf[8 * g + i]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pk[4 * g + i] = bf16x2{(bf16)pf[8 * g + 2 * i], (bf16)pf[8 * g + 2 * i + 1]};
+        for (int i = 0; i < 4; ++i) {
+          // (the tall D = 64 block: kAccMask is false, the x window is xpk)
+          const bf16x2 pr = bf16x2{(bf16)pf[8 * g + 2 * i], (bf16)pf[8 * g + 2 * i + 1]};
+          pk[4 * g + i] = __builtin_bit_cast(bf16x2, __builtin_bit_cast(uint32_t, pr) & xpk[4 * g + i]);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
       // row sums of the bf16 probabilities (dot2 with 1, 1): fp32 sums of
@@ -728,20 +730,13 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 #pragma unroll
         for (int u = 0; u < C::kScoresPerSlot; ++u) {
           const int e = i * C::kScoresPerSlot + u;
-          if constexpr (kAccMask) {
-            pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, mrow[e >> 3]));
-          } else {
-            S[e] = __builtin_fminf(__builtin_fminf(S[e], xlim[e]), rlim[e >> 3]);
-            pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, -m_run));
-          }
-          if (e & 1) {
-            pk[e >> 1] = bf16x2{(bf16)pf[e - 1], (bf16)pf[e]};
-            if constexpr (!kAccMask) l_tile = __builtin_amdgcn_fdot2_f32_bf16(pk[e >> 1], one2, l_tile, false);
-          }
+          static_assert(kAccMask, "the per-slot form runs with the accumulator-start x window");
+          pf[e] = fast_exp2(__builtin_fmaf(S[e], c2, mrow[e >> 3]));
+          if (e & 1) pk[e >> 1] = bf16x2{(bf16)pf[e - 1], (bf16)pf[e]};
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      if constexpr (kAccMask) l_tile = sum16(pf);
+      l_tile = sum16(pf);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -754,11 +749,13 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     // always lands here) -> raise m_run to the chunk max, rescale O and l and
     // recompute the chunk's probabilities.
     if (__builtin_amdgcn_ballot_w64(l_tile > kSumLimit || is_nan_bits(l_tile)) != 0) {
-      // (with kAccMask the scores carry the x window only; without it S is
-      // fully masked already)
+      // (with kAccMask the scores carry the x window; without it xpk holds it)
       float mx = -__builtin_inff();
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = __builtin_fmaxf(mx, !kAccMask || row_ok[i >> 3] ? S[i] : -__builtin_inff());
+      for (int i = 0; i < 16; ++i) {
+        const bool in = row_ok[i >> 3] && (kAccMask || ((xpk[i >> 1] >> ((i & 1) * 16)) & 1u) != 0);
+        mx = __builtin_fmaxf(mx, in ? S[i] : -__builtin_inff());
+      }
       const float mn = __builtin_fmaxf(m_run, halves_max(mx) * c2);
       const float alpha = fast_exp2(m_run - mn);
       m_run = mn;
@@ -778,12 +775,17 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
         }
         l_tile = sum16(pf);
       } else {
+        const float mr[2] = {row_ok[0] ? -mn : -__builtin_inff(), row_ok[1] ? -mn : -__builtin_inff()};
         l_tile = 0.f;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           bf16x8 pv;
 #pragma unroll
-          for (int r = 0; r < 8; ++r) pv[r] = (bf16)fast_exp2(__builtin_fmaf(S[8 * j + r], c2, -mn));
+          for (int r = 0; r < 8; ++r) pv[r] = (bf16)fast_exp2(__builtin_fmaf(S[8 * j + r], c2, mr[j]));
+          u32x4 w = __builtin_bit_cast(u32x4, pv);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) w[q] &= xpk[4 * j + q];
+          pv = __builtin_bit_cast(bf16x8, w);
           P[j] = pv;
           l_tile = sum8(pv, l_tile);
         }
