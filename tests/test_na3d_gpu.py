@@ -232,3 +232,39 @@ def test_na3d_config4_sampled_rows(gpu):
     ref_bf = O.na3d(q, k, v, (3, 7, 7), ty_rows=rows[:4], round_logits_bf16=True, round_weights_bf16=True)
     sel4 = tuple(np.array(rows[:4]).T)
     _check(o[0][sel4], ref_bf[0][sel4], "c4 rows vs bf16-logit reference")
+
+
+@pytest.mark.slow
+def test_na3d_stage5_sampled_rows(gpu):
+    """LTX-2.5 VAE stage-5 shape at full size: grid 33x88x160, window
+    (11,11,11), B=1 NH=4 D=64 (the 1 x 8 x 32 tall bricks); every query of
+    8 sampled (t, y) rows, borders and brick edges included, against the
+    oracle."""
+    from vidax_amd import _lib, neighborhood_attention_3d
+    _say("na3d stage 5 33x88x160 NH=4 D=64 (11,11,11) sampled rows")
+    B, T, H, W, NH = 1, 33, 88, 160, 4
+    q, k, v = O.make_na3d_inputs(B, T, H, W, NH, 64, 5)
+    out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), (11, 11, 11))
+    assert _lib.last_launch() == _expected_kernel(H, W, 11, 64), _lib.last_launch()
+    o = out.float().cpu().numpy()
+    rows = [(0, 0), (32, 87), (16, 7), (16, 8), (5, 44), (27, 80), (1, 86), (31, 3)]
+    ref = O.na3d(q, k, v, (11, 11, 11), ty_rows=rows)
+    sel = tuple(np.array(rows).T)
+    _check(o[0][sel], ref[0][sel], "stage-5 rows")
+
+
+@pytest.mark.slow
+def test_na3d_wide_window_sampled_rows(gpu):
+    """The per-wave kernel at the c4 grid with a (3,7,31) window, B=1 NH=24
+    D=128: every query of 6 sampled (t, y) rows against the oracle."""
+    from vidax_amd import _lib, neighborhood_attention_3d
+    _say("na3d 21x45x80 NH=24 (3,7,31) sampled rows")
+    B, T, H, W, NH = 1, 21, 45, 80, 24
+    q, k, v = O.make_na3d_inputs(B, T, H, W, NH, 128, 6)
+    out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), (3, 7, 31))
+    assert _lib.last_launch() == _expected_kernel(H, W, 31, 128), _lib.last_launch()
+    o = out.float().cpu().numpy()
+    rows = [(0, 0), (20, 44), (10, 3), (10, 4), (7, 41), (13, 22)]
+    ref = O.na3d(q, k, v, (3, 7, 31), ty_rows=rows)
+    sel = tuple(np.array(rows).T)
+    _check(o[0][sel], ref[0][sel], "wide-window rows")
