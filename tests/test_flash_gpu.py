@@ -266,8 +266,16 @@ def test_flash_config5_joint_sampled_rows(gpu):
     if p:
         valid[:, S - p:] = False
     out = masked_self_attention(q, k, v, key_valid=valid).reshape(1, S, 24, 128)
-    from vidax_amd import _lib
+    from vidax_amd import _lib, flash_attention
+    # a prefix mask at this size runs with kv_len alone
+    assert _lib.last_launch() == "flash_fwd_kernel<0, 128, 8>", _lib.last_launch()
+    # the general key-validity kernel on the same mask, at full size
+    kv_len = valid.to(torch.int32).sum(dim=1, dtype=torch.int32)
+    out_valid = flash_attention(q, k, v, scale=128 ** -0.5, kv_len=kv_len, key_valid=valid)
     assert _lib.last_launch() == "flash_fwd_kernel<1, 128, 8>", _lib.last_launch()
+    d = (out.float() - out_valid.float()).abs()
+    assert d.max().item() <= 1e-2 and d.mean().item() <= 1e-4, (d.max().item(), d.mean().item())
+    del out_valid, d
     rows = _residue_rows(S, 2, 4)
     assert len(rows) >= 512
     ref = O.attention_rows(_np(q), _np(k), _np(v), rows, key_valid=_np(valid).astype(bool))
@@ -705,3 +713,39 @@ def test_flash_key_bias_is_not_split(gpu):
     d = (out.float() - plain.float()).abs()
     print(f"  split vs unsplit: max {d.max().item():.3e} mean {d.mean().item():.3e}", flush=True)
     assert d.max().item() <= MAX_ABS and d.mean().item() <= MEAN_ABS
+
+
+@pytest.mark.parametrize("pattern", ["prefix", "holes", "none_valid"])
+def test_masked_self_attention_prefix_check(gpu, monkeypatch, pattern):
+    """Large masked_self_attention calls check whether key_valid is a prefix
+    (threshold lowered here to run it on a small shape): a prefix runs the
+    unmasked kernel with kv_len alone, anything else the validity kernel;
+    both agree with the oracle and with each other."""
+    from vidax_amd import _lib, attention, masked_self_attention
+    _say(f"masked_self_attention prefix check pattern={pattern}")
+    monkeypatch.setattr(attention, "_PREFIX_CHECK_MIN_PAIRS", 0)
+    B, S, H, D = 2, 700, 4, 128
+    q, k, v = _torch_inputs(B, S, S, H, 41, gpu)
+    valid = torch.ones((B, S), dtype=torch.bool, device=gpu)
+    if pattern == "prefix":
+        valid[0, 513:] = False
+        valid[1, 90:] = False
+    elif pattern == "holes":
+        valid[0, 100:130] = False
+        valid[1, 650:] = False
+    else:
+        valid[1, :] = False
+    out = masked_self_attention(q, k, v, key_valid=valid).reshape(B, S, H, D)
+    launched = _lib.last_launch()
+    mask_kind = 1 if pattern == "holes" else 0
+    assert launched.startswith(f"flash_fwd_kernel<{mask_kind}, ") or \
+        launched.startswith(f"flash_fwd_split_kernel<{mask_kind}, "), launched
+    rows = _rows(S, 64, 41)
+    ref = O.attention_rows(_np(q), _np(k), _np(v), rows, key_valid=_np(valid).astype(bool))
+    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"prefix check ({pattern}, {launched})")
+    monkeypatch.setattr(attention, "_PREFIX_CHECK_MIN_PAIRS", 1 << 62)
+    general = masked_self_attention(q, k, v, key_valid=valid).reshape(B, S, H, D)
+    assert _lib.last_launch().startswith("flash_fwd_kernel<1, ") or \
+        _lib.last_launch().startswith("flash_fwd_split_kernel<1, "), _lib.last_launch()
+    d = (out.float() - general.float()).abs()
+    assert d.max().item() <= 1e-2 and d.mean().item() <= 1e-4, (d.max().item(), d.mean().item())
