@@ -35,7 +35,8 @@ WORKLOADS = {
     "cross_L32760x512_B2": ("flash", dict(B=2, Sq=32760, Sk=512, H=40, seed=2, kv_len=(20, 512)),
                             "cross-attention B=2 H=40 Lq=32760 Lk=512, kv_len ~ U{20..512}"),
     "joint_L119056_H24": ("flash", dict(B=1, Sq=119056, Sk=119056, H=24, seed=4, tail_pad=(0, 200)),
-                          "joint self-attention B=1 H=24 S=33*45*80+256, last 0-200 keys masked"),
+                          "joint self-attention B=1 H=24 S=33*45*80+256, last 0-200 keys masked "
+                          "(masked_self_attention)"),
     "self_key_bias_L32760_H40": ("flash", dict(B=1, Sq=32760, Sk=32760, H=40, seed=1, key_bias_pad=(100, 300)),
                                  "self-attention B=1 H=40 L=32760 D=128 with a (B,1,1,Sk) additive key bias, "
                                  "-inf on a mid-sequence run of 100-300 keys (Cosmos3 text padding)"),
@@ -289,8 +290,15 @@ def main(argv=None):
         out = torch.empty_like(q)
         flops, bytes_ = _flash_work(p, valid_keys)
 
-        def step():
-            vidax_amd.flash_attention(q, k, v, out=out, **kw)
+        if "tail_pad" in p:
+            # HunyuanVideo's joint text+video attention, through its entry
+            # point (hunyuan_video/common/dit_layers.py:264-337): a key
+            # validity mask, valid keys a prefix
+            def step():
+                vidax_amd.masked_self_attention(q, k, v, key_valid=kw["key_valid"])
+        else:
+            def step():
+                vidax_amd.flash_attention(q, k, v, out=out, **kw)
     elif kind == "prologue":
         from vidax_amd.prologue import create_rope3d_freqs, qk_norm_rope
         g = torch.Generator(device=dev)
