@@ -749,3 +749,40 @@ def test_masked_self_attention_prefix_check(gpu, monkeypatch, pattern):
         _lib.last_launch().startswith("flash_fwd_split_kernel<1, "), _lib.last_launch()
     d = (out.float() - general.float()).abs()
     assert d.max().item() <= 1e-2 and d.mean().item() <= 1e-4, (d.max().item(), d.mean().item())
+
+
+@pytest.mark.parametrize("form", ["pure_hole", "pure_prefix", "general"])
+def test_dot_product_attention_key_bias_forms(gpu, monkeypatch, form):
+    """Large dot_product_attention calls hand a (B,1,1,Sk) key bias of only
+    0 / -inf (Cosmos3's padding bias) to the validity kernel, or, when its
+    valid keys are a prefix, to the unmasked kernel with kv_len; a bias with
+    other values stays a key bias. Threshold lowered here to run it on a
+    small shape; every form agrees with the oracle and with the key-bias
+    kernel."""
+    from vidax_amd import _lib, attention, dot_product_attention
+    _say(f"dot_product_attention key bias form={form}")
+    monkeypatch.setattr(attention, "_PREFIX_CHECK_MIN_PAIRS", 0)
+    B, S, H, D = 2, 640, 4, 128
+    q, k, v = _torch_inputs(B, S, S, H, 43, gpu)
+    bias = torch.zeros((B, S), dtype=torch.float32, device=gpu)
+    if form == "pure_hole":
+        bias[:, 200:260] = float("-inf")
+    elif form == "pure_prefix":
+        bias[0, 500:] = float("-inf")
+        bias[1, 37:] = float("-inf")
+    else:
+        bias = torch.randn((B, S), generator=torch.Generator(device=gpu).manual_seed(43), device=gpu)
+        bias[:, 300:333] = float("-inf")
+    out = dot_product_attention(q, k, v, bias=bias[:, None, None, :])
+    launched = _lib.last_launch()
+    want = {"pure_hole": 1, "pure_prefix": 0, "general": 2}[form]
+    assert launched.startswith(f"flash_fwd_kernel<{want}, ") or \
+        launched.startswith(f"flash_fwd_split_kernel<{want}, "), launched
+    rows = _rows(S, 64, 43)
+    ref = O.attention_rows(_np(q), _np(k), _np(v), rows, key_bias=_np(bias))
+    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"key bias form {form} ({launched})")
+    monkeypatch.setattr(attention, "_PREFIX_CHECK_MIN_PAIRS", 1 << 62)
+    as_bias = dot_product_attention(q, k, v, bias=bias[:, None, None, :])
+    assert _lib.last_launch().startswith("flash_fwd_kernel<2, "), _lib.last_launch()
+    d = (out.float() - as_bias.float()).abs()
+    assert d.max().item() <= 1e-2 and d.mean().item() <= 1e-4, (d.max().item(), d.mean().item())

@@ -233,6 +233,40 @@ def local_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return flash_attention(q, k, v, scale=sm_scale)
 
 
+# Calls of at least this many (batch, head, query, key) pairs look at their
+# key-only masks on the host first (a few device reductions and one
+# synchronisation: tens of microseconds against a kernel of milliseconds)
+# and hand the kernel the cheapest equivalent form: a key bias of only 0 and
+# -inf (Cosmos3's padding bias, cosmos3/dit_layers.py:124-130) becomes a
+# validity mask, and a validity mask whose valid keys are a prefix of each
+# batch item's keys (HunyuanVideo's joint attention) becomes kv_len alone.
+# The key-bias kernel ran ~14 % and the validity kernel ~4 % slower than the
+# unmasked one at these sizes. Skipped while the stream is being captured
+# into a graph.
+_PREFIX_CHECK_MIN_PAIRS = 1 << 34
+
+
+def _cheaper_key_masks(pairs: int, key_valid: Optional[torch.Tensor], key_bias: Optional[torch.Tensor],
+                       kv_len: Optional[torch.Tensor]):
+    """(key_valid, key_bias) in the cheapest form with the same meaning,
+    given kv_len (the last valid key + 1 of the combined masks)."""
+    if (key_valid is None and key_bias is None) or pairs < _PREFIX_CHECK_MIN_PAIRS or \
+            torch.cuda.is_current_stream_capturing():
+        return key_valid, key_bias
+    valid = key_valid
+    checks = []
+    if key_bias is not None:
+        bias_valid = key_bias == 0
+        checks.append((bias_valid | (key_bias == float("-inf"))).all())
+        valid = bias_valid if valid is None else (valid & bias_valid)
+    # (with kv_len from the combined masks: count of valid keys == last valid index + 1)
+    checks.append((valid.sum(dim=-1, dtype=torch.int32) == kv_len).all())
+    flags = torch.stack(checks).tolist()
+    if key_bias is not None and not flags[0]:
+        return key_valid, key_bias  # a bias with finite nonzero values
+    return (None if flags[-1] else valid), None
+
+
 def dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           bias: Optional[torch.Tensor] = None,
                           mask: Optional[torch.Tensor] = None,
@@ -243,7 +277,8 @@ def dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     `bias` and `mask` are broadcastable to (B, H, Sq, Sk), as in the
     reference. Key-only forms -- shape (B or 1, 1, 1, Sk), e.g. Cosmos3's
     (B, 1, 1, Sk) -inf padding bias -- run in the flash kernel's key-mask
-    path (the key loop is bounded by the last valid key). Head- or
+    path (the key loop is bounded by the last valid key; large calls get the
+    cheapest equivalent form, _cheaper_key_masks). Head- or
     query-dependent ones -- T5's relative-position bias, causal masks, the
     reference's `jax.nn.dot_product_attention` fallback -- run in the same
     kernel with a per-(query, key) bias (a boolean mask becomes 0 / -inf).
@@ -273,19 +308,10 @@ def dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             valid = key_valid if valid is None else (valid & key_valid)
     if valid is not None:
         kv_len = _last_valid_plus_one(valid)
+        if full is None:
+            key_valid, key_bias = _cheaper_key_masks(B * H * Sq * Sk, key_valid, key_bias, kv_len)
     return flash_attention(q, k, v, scale=sm_scale, kv_len=kv_len, key_valid=key_valid,
                            key_bias=key_bias, bias=full)
-
-
-# masked_self_attention calls of at least this many (query, key, head,
-# batch) pairs check on the host whether key_valid is a prefix of each
-# batch item's keys (two device reductions and one synchronisation, tens of
-# microseconds against a kernel of milliseconds); a prefix then runs the
-# kernel with kv_len alone, which skips the per-tile key-mask staging of
-# the general mask (HunyuanVideo's joint self-attention, 119,056 tokens: the
-# validity kernel ran about 4 % slower than the unmasked one). Skipped while
-# the stream is being captured into a graph.
-_PREFIX_CHECK_MIN_PAIRS = 1 << 34
 
 
 def masked_self_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -299,7 +325,7 @@ def masked_self_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     (q ids all 1, kv ids = key_valid; `dit_layers.py:183-186`). The reference
     documents valid keys as a prefix; any pattern is handled exactly here,
     and the key loop stops at the last valid key. Large calls whose mask is
-    a prefix run with kv_len alone (see _PREFIX_CHECK_MIN_PAIRS).
+    a prefix run with kv_len alone (_cheaper_key_masks).
     """
     del tp_sharded  # selects a shard_map wrapper in the reference; one GPU here
     _check_qkv(q, k, v)
@@ -311,12 +337,6 @@ def masked_self_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     else:
         kv = torch.as_tensor(key_valid, device=q.device).reshape(b, k.shape[1]).to(torch.bool)
         kv_len = _last_valid_plus_one(kv)
-        prefix = False
-        if b * h * s * k.shape[1] >= _PREFIX_CHECK_MIN_PAIRS and not torch.cuda.is_current_stream_capturing():
-            # valid keys form a prefix exactly when their count is the last valid index + 1
-            prefix = bool((kv.sum(dim=-1, dtype=torch.int32) == kv_len).all())
-        if prefix:
-            out = flash_attention(q, k, v, scale=scale, kv_len=kv_len)
-        else:
-            out = flash_attention(q, k, v, scale=scale, kv_len=kv_len, key_valid=kv)
+        kv, _ = _cheaper_key_masks(b * h * s * k.shape[1], kv, None, kv_len)
+        out = flash_attention(q, k, v, scale=scale, kv_len=kv_len, key_valid=kv)
     return out.reshape(b, s, h * d)
