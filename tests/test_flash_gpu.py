@@ -581,6 +581,7 @@ STREAM_CASES = [
     (1, 65536, 1024, 16, 128, None, 163),        # sixteen tiles, no kv_len
     (2, 32760, 512, 16, 64, [512, 20], 164),     # head dim 64
     (2, 16384, 256, 32, 128, [0, 0], 166),       # no keys at all: zero rows only
+    (8, 8192, 1024, 16, 128, [0, 1, 64, 1000, 0, 37, 1024, 700], 167),  # eight mixed batch items
 ]
 
 

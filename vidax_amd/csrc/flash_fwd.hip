@@ -733,15 +733,23 @@ void flash_stream_kernel(const FlashArgs a) {
   auto tiles_of = [](int kv) { return (kv + kBN - 1) / kBN; };
 
   // ---- this workgroup's items [i_lo, i_hi): item j of batch item b starts
-  // at work P_b + j * (n_b + 1), P_b the work of the batch items before b
+  // at work P_b + j * (n_b + kItemTiles), P_b the work of the batch items
+  // before b. An item's start and end (its q tile copy, the first tile's
+  // max, the output stores) cost about kItemTiles key tiles of the stream:
+  // with 1 instead of 3 the workgroups holding the short items of a batch
+  // with mixed kv_len finished late (same box: 32760 x 512 with kv_len
+  // 432 / 148 0.679 -> 0.634 ms, 32760 x 256 with 200 / 60 0.633 -> 0.540
+  // ms, 16384 x 1024 with 1000 / 700 / 300 / 30 1.394 -> 0.968 ms; equal
+  // items unchanged).
+  constexpr int kItemTiles = 3;
   int64_t W = 0;
-  for (int b = 0; b < a.B; ++b) W += (int64_t)per_b * (tiles_of(kv_end_of(b)) + 1);
+  for (int b = 0; b < a.B; ++b) W += (int64_t)per_b * (tiles_of(kv_end_of(b)) + kItemTiles);
   const int G = gridDim.x;
   const int chunk_id = (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8;
   auto first_item_at = [&](int64_t x) __attribute__((always_inline)) -> int {  // first item starting at or after work x
     int64_t P = 0;
     for (int b = 0; b < a.B; ++b) {
-      const int w = tiles_of(kv_end_of(b)) + 1;
+      const int w = tiles_of(kv_end_of(b)) + kItemTiles;
       const int64_t end = P + (int64_t)per_b * w;
       if (x < end) return b * per_b + (int)((x - P + w - 1) / w);
       P = end;
@@ -1295,8 +1303,10 @@ const char* flash_stream_kernel_name() {
 }
 
 // The persistent kernel: one workgroup per CU, a multiple of 8 (the XCDs).
-// A workgroup's items start within 1/groups of the work (items with keys
-// weigh at least 2), so it holds at most work / (2 * groups) + 1 of them;
+// A workgroup's items start within 1/groups of the kernel's work (n + 3 per
+// item of n <= T key tiles, T those of Sk: at most twice work = items *
+// (T + 1)), and items with keys weigh at least 4, so it holds at most
+// work / (2 * groups) + 1 of them;
 // grids whose workgroups could exceed the LDS table run the 128-query
 // kernel instead.
 template <int D>

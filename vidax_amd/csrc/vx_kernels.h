@@ -37,9 +37,10 @@ struct FlashArgs {
 };
 
 // Items (with keys) one workgroup of the persistent short-key kernel holds
-// in its LDS table. A workgroup's items start within 1/groups of the work
-// (key tiles + 1 per item; items with keys weigh at least 2), so it holds at
-// most work / (2 * groups) + 1 of them: the plan picks the kernel only for
+// in its LDS table. A workgroup's items start within 1/groups of the
+// kernel's work (key tiles + 3 per item, at most twice work = items * (T +
+// 1) with T the key tiles of Sk), and items with keys weigh at least 4, so
+// it holds at most work / (2 * groups) + 1 of them: the plan picks the kernel only for
 // grids with work / (2 * 256) + 2 <= kStreamTabMax, and the launcher checks
 // the same with the device's workgroup count.
 constexpr int kStreamTabMax = 1024;
