@@ -25,6 +25,9 @@ if ROOT not in sys.path:
 METRIC = "attention TFLOP/s + % bf16 MFMA peak at L=32760 H=40 D=128; ms/call"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
+# dense bf16 flop per shader clock cycle of the whole chip: 256 CUs x 4
+# matrix cores x 1024 flop (2.517 PFLOP/s at 2.4 GHz, quoted as 2.5)
+PEAK_BF16_FLOP_PER_CYCLE = 256 * 4 * 1024
 
 WORKLOADS = {
     # name: (kind, params, description)
@@ -38,8 +41,13 @@ WORKLOADS = {
                           "joint self-attention B=1 H=24 S=33*45*80+256, last 0-200 keys masked "
                           "(masked_self_attention)"),
     "self_key_bias_L32760_H40": ("flash", dict(B=1, Sq=32760, Sk=32760, H=40, seed=1, key_bias_pad=(100, 300)),
-                                 "self-attention B=1 H=40 L=32760 D=128 with a (B,1,1,Sk) additive key bias, "
-                                 "-inf on a mid-sequence run of 100-300 keys (Cosmos3 text padding)"),
+                                 "self-attention B=1 H=40 L=32760 D=128 with Cosmos3's (B,1,1,Sk) padding bias: "
+                                 "0 on valid keys, -inf on a mid-sequence run of 100-300 keys "
+                                 "(cosmos3/dit_layers.py:124-135), through dot_product_attention"),
+    "self_rand_key_bias_L32760_H40": ("flash", dict(B=1, Sq=32760, Sk=32760, H=40, seed=1, key_bias_pad=(100, 300),
+                                                    key_bias_randn=True),
+                                      "self-attention B=1 H=40 L=32760 D=128 with a general (B,1,1,Sk) additive "
+                                      "key bias: N(0,1) values, -inf on a mid-sequence run of 100-300 keys"),
     "t5_rel_bias_L512_H8_D64": ("flash", dict(B=2, Sq=512, Sk=512, H=8, D=64, seed=7, scale=1.0, t5_bias=True),
                                 "UMT5 encoder attention B=2 L=512 H=8 D=64, scale 1, (1,H,L,L) relative-position "
                                 "bias + (B,1,1,L) padding mask"),
@@ -106,7 +114,10 @@ def _flash_inputs(p, dev):
     if "key_bias_pad" in p:
         lo, hi = p["key_bias_pad"]
         n_pad = int(rng.integers(lo, hi + 1))
-        bias = torch.randn((B, Sk), generator=g, device=dev)
+        if p.get("key_bias_randn"):
+            bias = torch.randn((B, Sk), generator=g, device=dev)
+        else:
+            bias = torch.zeros((B, Sk), device=dev)
         s0 = Sk // 3
         bias[:, s0:s0 + n_pad] = float("-inf")
         kw["key_bias"] = bias
@@ -243,6 +254,57 @@ def _csrc_hash():
     return h.hexdigest()[:16]
 
 
+class _ClockStamps:
+    """The shader clock the chip held over the timed loop. The clock moves
+    with board power (a busy matrix core holds a lower clock, +-10 % between
+    boxes and between launches), so a kernel's rate depends on it. A stamp
+    (vx_debug_clock_stamp: 1024 one-wave workgroups, each storing its XCD,
+    its hardware id, the shader clock counter and the real-time counter) is
+    launched on the kernel's stream right before the loop and right after
+    it. The shader counter is kept per CU, so the stamps are paired by CU
+    (XCD, shader engine, CU): shader cycles passed / real time passed is that
+    CU's clock over the loop; the median over the CUs is reported."""
+
+    GROUPS = 1024
+
+    def __init__(self, dev):
+        import torch
+        self.buf = torch.zeros((2, 4 * self.GROUPS), dtype=torch.int64, device=dev)
+        self.khz = []
+
+    def stamp(self, i, stream):
+        import ctypes
+        from vidax_amd import _lib
+        khz = ctypes.c_int32(0)
+        rc = _lib.lib().vx_debug_clock_stamp(self.buf[i].data_ptr(), self.GROUPS, ctypes.byref(khz),
+                                             ctypes.c_void_p(stream.cuda_stream))
+        _lib.raise_for(rc)
+        self.khz.append(khz.value)
+
+    def result(self):
+        """{"mean", "median", "min", "max" (MHz over the CUs), "cus"} after a synchronize, or None."""
+        if len(self.khz) != 2 or self.khz[0] <= 0:
+            return None
+        a = self.buf.cpu().numpy().reshape(2, self.GROUPS, 4)
+        first = []
+        for i in range(2):
+            d = {}
+            for xcc, hw, cyc, real in a[i]:
+                d.setdefault((int(xcc), (int(hw) >> 8) & 0xFF), (int(cyc), int(real)))
+            first.append(d)
+        per = []
+        for key in sorted(set(first[0]) & set(first[1])):
+            (c0, r0), (c1, r1) = first[0][key], first[1][key]
+            real = (r1 - r0) / (self.khz[0] * 1e3)
+            if c1 > c0 and real > 0:
+                per.append((c1 - c0) / real / 1e6)
+        if not per:
+            return None
+        per.sort()
+        return {"median": per[len(per) // 2], "mean": sum(per) / len(per), "min": per[0], "max": per[-1],
+                "cus": len(per), "source": "s_memtime / s_memrealtime stamps around the timed loop, paired per CU"}
+
+
 def _copy_calibration(mib, steps):
     """A plain device copy of known size, timed the same way; profiled with the
     same counters it gives the bytes-per-KiB factor of FETCH_SIZE/WRITE_SIZE."""
@@ -296,6 +358,13 @@ def main(argv=None):
             # validity mask, valid keys a prefix
             def step():
                 vidax_amd.masked_self_attention(q, k, v, key_valid=kw["key_valid"])
+        elif "key_bias_pad" in p:
+            # a (B, 1, 1, Sk) key bias through dot_product_attention
+            # (src/vidax/core/attention.py:467-533), as Cosmos3 passes it
+            kb4 = kw["key_bias"][:, None, None, :]
+
+            def step():
+                vidax_amd.dot_product_attention(q, k, v, bias=kb4)
         else:
             def step():
                 vidax_amd.flash_attention(q, k, v, out=out, **kw)
@@ -358,13 +427,17 @@ def main(argv=None):
     kernel_name = _lib.last_launch()  # the kernel the step launched (the last one, for two launches)
     stream = torch.cuda.current_stream(dev)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    clock = _ClockStamps(dev)
     t0 = time.perf_counter()
+    clock.stamp(0, stream)
     ev[0].record(stream)
     for i in range(args.steps):
         step()
         ev[i + 1].record(stream)
+    clock.stamp(1, stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    sclk = clock.result()
     per = [ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]
     ms = sum(per) / len(per)
     tflops = flops / (ms * 1e-3) / 1e12
@@ -387,6 +460,17 @@ def main(argv=None):
         roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                     "traffic": _traffic(kernel_name, args.workload)}
+    # The shader clock held over the timed loop, and the work per clock cycle
+    # at that clock: flop/cycle over PEAK_BF16_FLOP_PER_CYCLE is the
+    # matrix-core fraction independent of the clock the box held.
+    roofline["sclk_mhz"] = round(sclk["median"], 1) if sclk else None
+    if sclk:
+        roofline["sclk"] = {k: (round(v, 1) if isinstance(v, float) else v) for k, v in sclk.items()}
+        cycles = ms * 1e-3 * sclk["median"] * 1e6
+        if flops:
+            roofline["flop_per_cycle"] = round(flops / cycles, 1)
+            roofline["frac_of_peak_at_sclk"] = round(flops / cycles / PEAK_BF16_FLOP_PER_CYCLE, 4)
+        roofline["bytes_per_cycle"] = round(bytes_ / cycles, 1)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = _cpu_baseline(kind, p, args.cpu_budget)

@@ -9,8 +9,10 @@
  * Layouts are the reference's: q/k/v/out are (B, S, H, D) bf16 for the flash
  * entry point and (B, T, Hs, W, NH, D) bf16 for the neighbourhood entry
  * point, with D (the head dim) contiguous. The library allocates nothing,
- * keeps no pointer after returning, never synchronises the stream, and may be
- * called concurrently from several host threads.
+ * keeps no pointer after returning and never synchronises the stream. Every
+ * entry point may be called concurrently from several host threads, except
+ * vx_flash_attn_noalloc_fwd: its calls share one static scratch array per
+ * device, so calls of it that overlap on one device race (see there).
  */
 #ifndef VX_ATTN_H_
 #define VX_ATTN_H_
@@ -26,7 +28,7 @@ extern "C" {
 #define VX_ERR_UNSUPPORTED 2      /* a valid request this build has no kernel for   */
 #define VX_ERR_LAUNCH 3           /* the HIP runtime refused the launch             */
 
-/* Version of this ABI (major * 10000 + minor * 100 + patch): 1.6.0. */
+/* Version of this ABI (major * 10000 + minor * 100 + patch): 1.7.0. */
 int32_t vx_abi_version(void);
 
 /* Message describing the most recent failure on the calling thread ("" if none). */
@@ -366,6 +368,20 @@ const char* vx_last_launch(void);
  * with a message naming the injection. 0 turns it off. Process-wide.
  */
 void vx_debug_inject_error(int32_t code);
+
+/*
+ * Measurement hook (no counterpart in the reference; not part of the
+ * attention path): launches n_groups (1..4096) one-wave workgroups on
+ * `stream`, each storing four uint64 at out[4*g]: the XCD it ran on, its
+ * hardware id (HW_REG_HW_ID: shader engine, CU, SIMD, wave slot), the
+ * shader clock counter (read per CU) and the real-time counter, read when it
+ * runs. *wall_clock_khz receives the real-time counter's rate. Two stamps
+ * around a run of kernels on one stream give, per CU found in both, the
+ * shader cycles and the wall time that passed: the clock the chip held
+ * under that load. `out` is device memory, 8-byte aligned, of 4 * n_groups
+ * uint64.
+ */
+int32_t vx_debug_clock_stamp(uint64_t* out, int32_t n_groups, int32_t* wall_clock_khz, void* stream);
 
 #ifdef __cplusplus
 }

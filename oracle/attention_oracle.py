@@ -255,6 +255,55 @@ def na3d_loops(q, k, v, kernel_size, scale=1.0):
 
 
 # ------------------------------------------------------------ inputs
+def na3d_dense(q, k, v, kernel_size, scale=1.0, acc=np.float64, ty_rows=None):
+    """na3d restated for whole grids: the same windows, computed per (t, y)
+    query row as two dense matrix products over the row's key box.
+
+    For query row (t, y) every query's window lies in the box of key rows
+    it[t] x ih[y] (all W x positions); each query (x) keeps the kw' x
+    positions iw[x] of every box row, so masking the rest to -inf before the
+    softmax gives exactly its kt'*kh'*kw' keys (`diffusion_vae.py:152-234`).
+    The products run on BLAS, over blocks of 16 queries along x (window
+    starts grow with x, so a block's windows span x positions [start(x0),
+    start(x1 - 1) + kw')), which makes the whole 21x45x80x24 grid a matter
+    of seconds. `ty_rows` as in na3d (other rows left at zero).
+    """
+    q = np.asarray(q)
+    k = np.asarray(k)
+    v = np.asarray(v)
+    B, T, Hs, W, NH, D = q.shape
+    kt, kh, kw = kernel_size
+    it = window_indices(T, kt)
+    ih = window_indices(Hs, kh)
+    iw = window_indices(W, kw)
+    kw_ = iw.shape[1]
+    nbox = it.shape[1] * ih.shape[1]
+    XB = 16
+    out = np.zeros(q.shape, dtype=acc)
+    rows = [(t, y) for t in range(T) for y in range(Hs)] if ty_rows is None else list(ty_rows)
+    for b in range(B):
+        kb = np.ascontiguousarray(np.moveaxis(k[b], 3, 0), dtype=acc)        # (NH, T, Hs, W, D)
+        vb = np.ascontiguousarray(np.moveaxis(v[b], 3, 0), dtype=acc)
+        for t, y in rows:
+            qq = np.ascontiguousarray(np.moveaxis(q[b, t, y], 1, 0), dtype=acc)   # (NH, W, D)
+            tt, yy = it[t][:, None], ih[y][None, :]
+            kbox = kb[:, tt, yy]                                                # (NH, kt', kh', W, D)
+            vbox = vb[:, tt, yy]
+            for x0 in range(0, W, XB):
+                x1 = min(W, x0 + XB)
+                lo, hi = int(iw[x0, 0]), int(iw[x1 - 1, 0]) + kw_
+                kk = kbox[:, :, :, lo:hi].reshape(NH, nbox * (hi - lo), D)
+                vv = vbox[:, :, :, lo:hi].reshape(NH, nbox * (hi - lo), D)
+                # allowed[x, j]: box column j (x position lo + j % (hi - lo)) is in query x's window
+                xin = np.zeros((x1 - x0, hi - lo), dtype=bool)
+                xin[np.arange(x1 - x0)[:, None], iw[x0:x1] - lo] = True
+                allowed = np.tile(xin, (1, nbox))
+                logits = np.matmul(qq[:, x0:x1], np.swapaxes(kk, 1, 2)) * acc(scale)   # (NH, xb, box keys)
+                w = _softmax_rows(np.where(allowed[None], logits, -np.inf))
+                out[b, t, y, x0:x1] = np.moveaxis(np.matmul(w, vv), 0, 1)              # (xb, NH, D)
+    return out
+
+
 def _normal_bf16(rng, shape):
     return bf16_round(rng.standard_normal(shape, dtype=np.float32))
 

@@ -32,7 +32,7 @@ def test_header_symbols_are_exported():
 
 
 def test_abi_version():
-    assert _lib.lib().vx_abi_version() == 10600
+    assert _lib.lib().vx_abi_version() == 10700
 
 
 def _flash_check(**kw):
@@ -296,7 +296,9 @@ def test_na3d_kernel_name_follows_the_launch_rule():
     """The C ABI's NA launch plan, by the clamped x window."""
     from vidax_amd.natten import na3d_kernel_name
     assert na3d_kernel_name(80, 7) == "na3d_pipe_kernel<16, 128>"
-    assert na3d_kernel_name(80, 9, 64) == "na3d_pipe_kernel<16, 64>"
+    assert na3d_kernel_name(80, 9, 64, height=4) == "na3d_pipe_kernel<16, 64>"   # 8x80 vs 4x96
+    with pytest.raises(ValueError, match="height"):
+        na3d_kernel_name(80, 9, 64)   # the height decides here
     # head dim 64, kw' <= 9: the tall bricks unless they pad the y-x plane more
     assert na3d_kernel_name(80, 7, 64, height=45) == "na3d_tall_kernel<64>"    # 48x80 vs 48x96
     assert na3d_kernel_name(80, 5, 64, height=44) == "na3d_tall_kernel<64>"    # 48x80 vs 44x96
@@ -483,3 +485,41 @@ def test_ws_fwd_rejects_before_launch():
     assert L.vx_flash_attn_ws_fwd(*args, A, -1, None) == _lib.VX_ERR_INVALID_ARGUMENT
     args[12] = 96
     assert L.vx_flash_attn_ws_fwd(*args, A, 1024, None) == _lib.VX_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("D,code", [(64, _lib.VX_OK), (128, _lib.VX_OK),
+                                    (80, _lib.VX_ERR_UNSUPPORTED), (384, _lib.VX_ERR_UNSUPPORTED)])
+def test_flash_head_dim_check_for_drop_in_branch(D, code):
+    """The trace-time check a drop-in branch makes before choosing the kernel:
+    CLIP vision runs dot_product_attention at D=80 (16 heads of dim 1280,
+    wan/wan2_1/clip_vision.py:36-46) and the Wan2.1 VAE's middle attention at
+    one head of D=384 (wan/common/vae_layers.py:100-110); both keep the
+    reference's jax.nn path. The check is host-only (no GPU)."""
+    import vidax_amd
+    from vidax_amd.attention import _require_supported
+    # CLIP: 257 tokens x 16 heads; VAE middle block: one 60x104 frame, 1 head
+    B, S, H = (1, 257, 16) if D == 80 else (1, 6240, 1) if D == 384 else (1, 4096, 8)
+    assert _flash_check(B=B, Sq=S, Sk=S, H=H, D=D) == code
+    if code == _lib.VX_ERR_UNSUPPORTED:
+        assert "head_dim" in _lib.last_error()
+    assert vidax_amd.flash_supported(B, S, S, H, D) == (code == _lib.VX_OK)
+    assert _lib.flash_shape_check(B, S, S, H, D)[0] == code
+    if code == _lib.VX_OK:
+        _require_supported(B, S, S, H, D)
+    else:
+        with pytest.raises(NotImplementedError, match=rf"head_dim {D} .*jax\.nn\.dot_product_attention.*flash_supported"):
+            _require_supported(B, S, S, H, D)
+
+
+def test_flash_kernel_name_with_the_key_split():
+    """With the device's compute-unit count the name follows the workspace
+    entry point that flash_attention calls: the key-split kernel for grids
+    whose last round would leave most of the device idle, never with a key
+    or full bias (those never split)."""
+    from vidax_amd.attention import flash_kernel_name
+    assert flash_kernel_name(1, 7800, 7800, 12) == "flash_fwd_kernel<0, 128, 4>"
+    assert flash_kernel_name(1, 7800, 7800, 12, num_cus=256) == "flash_fwd_split_kernel<0, 128, 4>"
+    assert flash_kernel_name(1, 7800, 7800, 12, 128, 1, num_cus=256) == "flash_fwd_split_kernel<1, 128, 4>"
+    assert flash_kernel_name(1, 7800, 7800, 12, 128, 2, num_cus=256) == "flash_fwd_kernel<2, 128, 4>"
+    assert flash_kernel_name(1, 32760, 32760, 40, num_cus=256) == "flash_fwd_kernel<0, 128, 8>"   # 5120 tiles
+    assert flash_kernel_name(2, 32760, 512, 40, num_cus=256) == "flash_stream_kernel<128>"

@@ -75,6 +75,25 @@ def test_flash_small(gpu, B, Sq, Sk, H, seed, mask):
     _check(out, ref, "oracle")
 
 
+@pytest.mark.parametrize("B,Sq,Sk,H,D,scale,seed", [
+    (1, 300, 777, 3, 128, None, 20),     # default scale 1/sqrt(D)
+    (2, 200, 129, 2, 64, 0.3, 21),       # explicit scale, head dim 64
+    (1, 2048, 2048, 8, 128, 1.0, 22),    # scale 1
+])
+def test_local_attention(gpu, B, Sq, Sk, H, D, scale, seed):
+    """local_attention (`src/vidax/core/attention.py:321-338`): the unmasked
+    kernel with the reference's scale rule (1/sqrt(D) unless given)."""
+    from vidax_amd import _lib, local_attention
+    _say(f"local_attention B={B} Sq={Sq} Sk={Sk} H={H} D={D} scale={scale}")
+    q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, D, seed)
+    out = local_attention(_t(q, gpu), _t(k, gpu), _t(v, gpu), scale=scale)
+    torch.cuda.synchronize()
+    assert _lib.last_launch().startswith(("flash_fwd_kernel<0,", "flash_fwd_split_kernel<0,")), _lib.last_launch()
+    assert out.shape == (B, Sq, H, D) and out.dtype == torch.bfloat16
+    ref = O.attention(q, k, v, scale=D ** -0.5 if scale is None else scale)
+    _check(out, ref, "oracle")
+
+
 ROW_SHIFTS = [-1000.0, -120.0, 200.0, 1000.0]
 
 
@@ -636,6 +655,48 @@ def test_flash_stream_kernel_strided_views(gpu):
     assert torch.equal(out, out_c)
 
 
+def test_flash_stream_kernel_last_row_after_late_rescale(gpu):
+    """Ragged Sq: the last 256-query tile holds queries past Sq, whose lanes
+    repeat row Sq-1's query. Only the wave that owns row Sq-1 may store it.
+    Built so that the owner's wave takes the rare rescale in the last key
+    tile (another of its queries, row Sq-2, scores one late key far above
+    everything), and row Sq-1 itself has a new, moderate maximum in that
+    tile: the owner raises row Sq-1's reference point there, the waves that
+    only hold copies of row Sq-1 do not, so their bf16 probabilities (and
+    stores) would differ. Every row must equal, bit for bit, the 128-query
+    kernel's (same waves: each row stored once, by its owner)."""
+    from vidax_amd import _lib, dot_product_attention, flash_attention
+    B, Sq, Sk, H, D, kv, seed = 1, 65436, 512, 16, 128, 500, 168
+    _say(f"flash stream ragged Sq={Sq} late rescale in the owner's wave, H={H} kv_len={kv}")
+    g = torch.Generator(device=gpu)
+    g.manual_seed(seed)
+    q, k, v = (torch.randn((B, n, H, D), generator=g, device=gpu, dtype=torch.float32) for n in (Sq, Sk, Sk))
+    js = 470                                          # a key in the last tile (keys 448..499)
+    ks = k[0, js]                                     # (H, D)
+    nrm2 = (ks * ks).sum(-1, keepdim=True)
+    scale = D ** -0.5
+    # row Sq-2: logit 20 on key js (2^24 above its reference point: the rare path)
+    q[0, Sq - 2] = ks * (20.0 / (scale * nrm2))
+    # row Sq-1: logit 4.5 on key js, all its other logits ~N(0, 0.4^2): a new
+    # maximum in the last tile, probability sum well below 2^8 (no rescale of its own)
+    q[0, Sq - 1] = ks * (4.5 / (scale * nrm2))
+    q, k, v = (x.to(torch.bfloat16) for x in (q, k, v))
+    kv_t = torch.tensor([kv], dtype=torch.int32, device=gpu)
+    out = flash_attention(q, k, v, kv_len=kv_t)
+    torch.cuda.synchronize()
+    assert _lib.last_launch() == "flash_stream_kernel<128>", _lib.last_launch()
+    valid = torch.arange(Sk, device=gpu)[None, :] < kv_t[:, None]
+    out2 = dot_product_attention(q, k, v, mask=valid[:, None, None, :])
+    torch.cuda.synchronize()
+    assert _lib.last_launch() == "flash_fwd_kernel<1, 128, 4>", _lib.last_launch()
+    tail = slice(Sq - 64, Sq)
+    print(f"  last rows equal: {torch.equal(out[:, tail], out2[:, tail])}", flush=True)
+    assert torch.equal(out, out2)
+    rows = np.array([0, Sq - 300, Sq - 3, Sq - 2, Sq - 1])
+    ref = O.attention_rows(_np(q), _np(k), _np(v), rows, kv_len=np.array([kv], np.int32))
+    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, "stream ragged rows")
+
+
 # ------------------------------------------------ key split of the last round
 def _plain_flash(q, k, v, kw, scale=None):
     """The same call through vx_flash_attn_fwd, which never splits."""
@@ -717,14 +778,15 @@ def test_flash_key_bias_is_not_split(gpu):
 
 
 @pytest.mark.parametrize("pattern", ["prefix", "holes", "none_valid"])
-def test_masked_self_attention_prefix_check(gpu, monkeypatch, pattern):
-    """Large masked_self_attention calls check whether key_valid is a prefix
-    (threshold lowered here to run it on a small shape): a prefix runs the
-    unmasked kernel with kv_len alone, anything else the validity kernel;
-    both agree with the oracle and with each other."""
-    from vidax_amd import _lib, attention, masked_self_attention
-    _say(f"masked_self_attention prefix check pattern={pattern}")
-    monkeypatch.setattr(attention, "_PREFIX_CHECK_MIN_PAIRS", 0)
+def test_masked_self_attention_key_valid_patterns(gpu, pattern):
+    """masked_self_attention hands key_valid to the validity kernel with
+    kv_len = last valid key + 1 and never inspects the mask on the host; the
+    kernel classifies each 64-key tile (all valid: unmasked path). A prefix
+    mask must give the same result as kv_len alone (the unmasked kernel), and
+    every pattern agrees with the oracle."""
+    from vidax_amd import _lib, flash_attention, masked_self_attention
+    from vidax_amd.attention import _last_valid_plus_one
+    _say(f"masked_self_attention key_valid pattern={pattern}")
     B, S, H, D = 2, 700, 4, 128
     q, k, v = _torch_inputs(B, S, S, H, 41, gpu)
     valid = torch.ones((B, S), dtype=torch.bool, device=gpu)
@@ -738,31 +800,30 @@ def test_masked_self_attention_prefix_check(gpu, monkeypatch, pattern):
         valid[1, :] = False
     out = masked_self_attention(q, k, v, key_valid=valid).reshape(B, S, H, D)
     launched = _lib.last_launch()
-    mask_kind = 1 if pattern == "holes" else 0
-    assert launched.startswith(f"flash_fwd_kernel<{mask_kind}, ") or \
-        launched.startswith(f"flash_fwd_split_kernel<{mask_kind}, "), launched
+    assert launched.startswith("flash_fwd_kernel<1, ") or launched.startswith("flash_fwd_split_kernel<1, "), launched
     rows = _rows(S, 64, 41)
     ref = O.attention_rows(_np(q), _np(k), _np(v), rows, key_valid=_np(valid).astype(bool))
-    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"prefix check ({pattern}, {launched})")
-    monkeypatch.setattr(attention, "_PREFIX_CHECK_MIN_PAIRS", 1 << 62)
-    general = masked_self_attention(q, k, v, key_valid=valid).reshape(B, S, H, D)
-    assert _lib.last_launch().startswith("flash_fwd_kernel<1, ") or \
-        _lib.last_launch().startswith("flash_fwd_split_kernel<1, "), _lib.last_launch()
-    d = (out.float() - general.float()).abs()
-    assert d.max().item() <= 1e-2 and d.mean().item() <= 1e-4, (d.max().item(), d.mean().item())
+    _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"key_valid {pattern} ({launched})")
+    if pattern != "holes":
+        by_len = flash_attention(q, k, v, kv_len=_last_valid_plus_one(valid))
+        torch.cuda.synchronize()
+        assert _lib.last_launch().startswith(("flash_fwd_kernel<0, ", "flash_fwd_split_kernel<0, "))
+        same = torch.equal(out, by_len)
+        d = (out.float() - by_len.float()).abs()
+        print(f"  validity kernel vs kv_len alone: equal={same} max {d.max().item():.3e}", flush=True)
+        assert d.max().item() <= 1e-2 and d.mean().item() <= 1e-4, (d.max().item(), d.mean().item())
 
 
-@pytest.mark.parametrize("form", ["pure_hole", "pure_prefix", "general"])
-def test_dot_product_attention_key_bias_forms(gpu, monkeypatch, form):
-    """Large dot_product_attention calls hand a (B,1,1,Sk) key bias of only
-    0 / -inf (Cosmos3's padding bias) to the validity kernel, or, when its
-    valid keys are a prefix, to the unmasked kernel with kv_len; a bias with
-    other values stays a key bias. Threshold lowered here to run it on a
-    small shape; every form agrees with the oracle and with the key-bias
-    kernel."""
-    from vidax_amd import _lib, attention, dot_product_attention
+@pytest.mark.parametrize("form", ["pure_hole", "pure_prefix", "general", "zero"])
+def test_dot_product_attention_key_bias_forms(gpu, form):
+    """A (B,1,1,Sk) key bias stays a key bias (no host inspection): the
+    kernel starts the accumulators of all-zero bias tiles at zero and adds
+    the bias elsewhere. Cosmos3's padding bias (0 / -inf: a hole, or a valid
+    prefix) must equal the same keys given as a validity mask; a general
+    bias and an all-zero one agree with the oracle (the zero bias with the
+    unmasked kernel)."""
+    from vidax_amd import _lib, dot_product_attention
     _say(f"dot_product_attention key bias form={form}")
-    monkeypatch.setattr(attention, "_PREFIX_CHECK_MIN_PAIRS", 0)
     B, S, H, D = 2, 640, 4, 128
     q, k, v = _torch_inputs(B, S, S, H, 43, gpu)
     bias = torch.zeros((B, S), dtype=torch.float32, device=gpu)
@@ -771,19 +832,20 @@ def test_dot_product_attention_key_bias_forms(gpu, monkeypatch, form):
     elif form == "pure_prefix":
         bias[0, 500:] = float("-inf")
         bias[1, 37:] = float("-inf")
-    else:
+    elif form == "general":
         bias = torch.randn((B, S), generator=torch.Generator(device=gpu).manual_seed(43), device=gpu)
         bias[:, 300:333] = float("-inf")
     out = dot_product_attention(q, k, v, bias=bias[:, None, None, :])
     launched = _lib.last_launch()
-    want = {"pure_hole": 1, "pure_prefix": 0, "general": 2}[form]
-    assert launched.startswith(f"flash_fwd_kernel<{want}, ") or \
-        launched.startswith(f"flash_fwd_split_kernel<{want}, "), launched
+    assert launched.startswith("flash_fwd_kernel<2, "), launched
     rows = _rows(S, 64, 43)
     ref = O.attention_rows(_np(q), _np(k), _np(v), rows, key_bias=_np(bias))
     _check(out[:, torch.from_numpy(rows).to(gpu)], ref, f"key bias form {form} ({launched})")
-    monkeypatch.setattr(attention, "_PREFIX_CHECK_MIN_PAIRS", 1 << 62)
-    as_bias = dot_product_attention(q, k, v, bias=bias[:, None, None, :])
-    assert _lib.last_launch().startswith("flash_fwd_kernel<2, "), _lib.last_launch()
-    d = (out.float() - as_bias.float()).abs()
-    assert d.max().item() <= 1e-2 and d.mean().item() <= 1e-4, (d.max().item(), d.mean().item())
+    if form != "general":
+        as_mask = dot_product_attention(q, k, v, mask=(bias > float("-inf"))[:, None, None, :])
+        torch.cuda.synchronize()
+        assert _lib.last_launch().startswith(("flash_fwd_kernel<1, ", "flash_fwd_split_kernel<1, "))
+        d = (out.float() - as_mask.float()).abs()
+        print(f"  key bias vs validity mask: equal={torch.equal(out, as_mask)} max {d.max().item():.3e}",
+              flush=True)
+        assert d.max().item() <= 1e-2 and d.mean().item() <= 1e-4, (d.max().item(), d.mean().item())

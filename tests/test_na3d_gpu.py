@@ -212,23 +212,23 @@ def test_na3d_deterministic(gpu):
 
 
 @pytest.mark.slow
-def test_na3d_config4_sampled_rows(gpu):
-    """Config shape: grid 21x45x80, window (3,7,7), B=1 NH=24 D=128; every
-    query of 14 sampled (t, y) rows (borders included) against the oracle."""
+def test_na3d_config4_whole_grid(gpu):
+    """Config shape: grid 21x45x80, window (3,7,7), B=1 NH=24 D=128: every
+    query of the grid against the oracle (its dense per-row form, fp32 on
+    BLAS), and 14 (t, y) rows against the reference's own dtype points."""
     from vidax_amd import neighborhood_attention_3d
-    _say("na3d c4 21x45x80 NH=24 (3,7,7) sampled rows")
+    _say("na3d c4 21x45x80 NH=24 (3,7,7) whole grid")
     B, T, H, W, NH = 1, 21, 45, 80, 24
     q, k, v = O.make_na3d_inputs(B, T, H, W, NH, 128, 3)
     out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), (3, 7, 7))
     from vidax_amd import _lib
     assert _lib.last_launch() == "na3d_pipe_kernel<16, 128>", _lib.last_launch()
     o = out.float().cpu().numpy()
+    ref = O.na3d_dense(q, k, v, (3, 7, 7), acc=np.float32)
+    _check(o, ref, "c4 whole grid")
+    # the reference's own dtype points (bf16 logits and weights) stay within the bar too
     rows = [(0, 0), (0, 44), (20, 0), (20, 44), (1, 1), (10, 22), (10, 3), (19, 43),
             (5, 40), (15, 2), (2, 21), (18, 30), (11, 44), (9, 0)]
-    ref = O.na3d(q, k, v, (3, 7, 7), ty_rows=rows)
-    sel = tuple(np.array(rows).T)
-    _check(o[0][sel], ref[0][sel], "c4 rows")
-    # the reference's own dtype points (bf16 logits and weights) stay within the bar too
     ref_bf = O.na3d(q, k, v, (3, 7, 7), ty_rows=rows[:4], round_logits_bf16=True, round_weights_bf16=True)
     sel4 = tuple(np.array(rows[:4]).T)
     _check(o[0][sel4], ref_bf[0][sel4], "c4 rows vs bf16-logit reference")
@@ -238,8 +238,9 @@ def test_na3d_config4_sampled_rows(gpu):
 def test_na3d_stage5_sampled_rows(gpu):
     """LTX-2.5 VAE stage-5 shape at full size: grid 33x88x160, window
     (11,11,11), B=1 NH=4 D=64 (the 1 x 8 x 32 tall bricks); every query of
-    8 sampled (t, y) rows, borders and brick edges included, against the
-    oracle."""
+    64 sampled (t, y) rows against the oracle: 8 rows for each y mod 8 (each
+    wave's position in its 8-row brick), the t and y borders included; a row
+    holds every x brick of the grid."""
     from vidax_amd import _lib, neighborhood_attention_3d
     _say("na3d stage 5 33x88x160 NH=4 D=64 (11,11,11) sampled rows")
     B, T, H, W, NH = 1, 33, 88, 160, 4
@@ -247,10 +248,18 @@ def test_na3d_stage5_sampled_rows(gpu):
     out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), (11, 11, 11))
     assert _lib.last_launch() == _expected_kernel(H, W, 11, 64), _lib.last_launch()
     o = out.float().cpu().numpy()
-    rows = [(0, 0), (32, 87), (16, 7), (16, 8), (5, 44), (27, 80), (1, 86), (31, 3)]
-    ref = O.na3d(q, k, v, (11, 11, 11), ty_rows=rows)
+    rng = np.random.default_rng(55)
+    rows = {(0, 0), (32, 87), (16, 7), (16, 8), (5, 44), (27, 80), (1, 86), (31, 3)}
+    for r in range(8):
+        ys = [y for y in range(H) if y % 8 == r]
+        ts = [0, T - 1] + [int(x) for x in rng.choice(np.arange(1, T - 1), size=6, replace=False)]
+        yy = [ys[0], ys[-1]] + [int(x) for x in rng.choice(ys[1:-1], size=6, replace=False)]
+        rows.update(zip(ts, yy))
+    rows = sorted(rows)
+    assert len(rows) >= 64 and len({y % 8 for _, y in rows}) == 8
+    ref = O.na3d_dense(q, k, v, (11, 11, 11), acc=np.float32, ty_rows=rows)
     sel = tuple(np.array(rows).T)
-    _check(o[0][sel], ref[0][sel], "stage-5 rows")
+    _check(o[0][sel], ref[0][sel], f"stage-5 {len(rows)} rows")
 
 
 @pytest.mark.slow

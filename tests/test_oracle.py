@@ -196,6 +196,28 @@ def test_na3d_matches_brute_force(shape, ks):
                                rtol=1e-10, atol=1e-12)
 
 
+@pytest.mark.parametrize("shape,ks", [
+    ((1, 3, 4, 5, 2, 8), (3, 3, 3)),
+    ((1, 2, 5, 6, 1, 8), (3, 5, 2)),   # kt clamped to T = 2, even kw
+    ((2, 4, 3, 3, 1, 4), (1, 7, 7)),   # kh, kw clamped
+    ((1, 5, 2, 7, 1, 4), (4, 1, 6)),
+    ((1, 4, 9, 11, 3, 8), (3, 7, 7)),  # the (3, 7, 7) window with borders on every side
+])
+def test_na3d_dense_matches_gather_and_brute_force(shape, ks):
+    """The dense per-row form (two matrix products over each query row's key
+    box, out-of-window box keys masked) used for whole-grid GPU checks
+    equals the window-gather form and the brute force."""
+    rng = np.random.default_rng(9)
+    q, k, v = (rng.standard_normal(shape) for _ in range(3))
+    dense = O.na3d_dense(q, k, v, ks, scale=0.7)
+    np.testing.assert_allclose(dense, O.na3d(q, k, v, ks, scale=0.7), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dense, O.na3d_loops(q, k, v, ks, scale=0.7), rtol=1e-10, atol=1e-12)
+    rows = [(0, 0), (shape[1] - 1, shape[2] - 1)]
+    part = O.na3d_dense(q, k, v, ks, scale=0.7, ty_rows=rows)
+    sel = tuple(np.array(rows).T)
+    np.testing.assert_allclose(part[:, sel[0], sel[1]], dense[:, sel[0], sel[1]], rtol=1e-12, atol=1e-14)
+
+
 def test_na3d_window_one_is_identity():
     rng = np.random.default_rng(7)
     q, k, v = (rng.standard_normal((1, 3, 4, 5, 2, 8)) for _ in range(3))

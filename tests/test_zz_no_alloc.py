@@ -62,3 +62,38 @@ def test_noalloc_matches_workspace_entry(gpu):
         err = np.abs(out_na[:, torch.from_numpy(rows).to(gpu)].float().cpu().numpy() - ref)
         print(f"  vs oracle: max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
         assert err.max() <= 2e-2 and err.mean() <= 2e-3
+
+
+def test_noalloc_under_graph_capture(gpu):
+    """The use the entry point exists for: captured into a HIP graph (torch's
+    CUDAGraph, global capture mode, in which a device allocation inside the
+    capture fails) after one eager warm-up call, then replayed. Between
+    replays the program runs its own eager work, including an eager call on
+    a smaller problem that overwrites the shared scratch; every replay must
+    equal the eager result bit for bit."""
+    B, Sq, Sk, H, seed = 1, 7800, 7800, 12, 182   # splits 220 of 732 items into the scratch
+    print(f"[case] noalloc graph capture B={B} Sq={Sq} Sk={Sk} H={H}", flush=True)
+    q, k, v, _ = O.make_flash_inputs(B, Sq, Sk, H, 128, seed)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(gpu).to(torch.bfloat16)
+    tq, tk, tv = t(q), t(k), t(v)
+    out_eager = torch.empty_like(tq)
+    assert _call("noalloc", tq, tk, tv, out_eager) == "flash_fwd_split_kernel<0, 128, 4>"  # warm-up
+    torch.cuda.synchronize()
+    # a smaller problem whose split also goes through the scratch
+    q2, k2, v2, _ = O.make_flash_inputs(2, 700, 2100, 2, 128, seed + 1)
+    sq2, sk2, sv2 = t(q2), t(k2), t(v2)
+    out2 = torch.empty_like(sq2)
+
+    out_g = torch.empty_like(tq)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _call("noalloc", tq, tk, tv, out_g)
+    for r in range(4):
+        out_g.fill_(7.0)                               # eager work between replays
+        _call("noalloc", sq2, sk2, sv2, out2)          # dirties the scratch
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        same = torch.equal(out_g, out_eager)
+        print(f"  replay {r}: equal to eager = {same}", flush=True)
+        assert same, f"replay {r} differs from the eager call"

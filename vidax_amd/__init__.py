@@ -11,7 +11,7 @@ and the q/k prologue in front of them:
   na3d_qk_norm_rope                       (src/vidax/models/ltx2_5/diffusion_vae.py)
 all backed by libvx_attn.so (C ABI: include/vx_attn.h).
 """
-from .attention import (dot_product_attention, flash_attention, local_attention,
+from .attention import (dot_product_attention, flash_attention, flash_supported, local_attention,
                         masked_self_attention)
 from .natten import na3d_block_attention, neighborhood_attention_3d
 from .prologue import (apply_abs_rope3d, apply_rope3d, create_abs_rope3d_freqs, create_rope3d_freqs,
@@ -20,6 +20,7 @@ from .prologue import (apply_abs_rope3d, apply_rope3d, create_abs_rope3d_freqs, 
 __all__ = [
     "dot_product_attention",
     "flash_attention",
+    "flash_supported",
     "local_attention",
     "masked_self_attention",
     "neighborhood_attention_3d",

@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "vx_flash_attn_workspace_size",
     "vx_flash_attn_split_plan",
     "vx_flash_attn_noalloc_fwd",
+    "vx_debug_clock_stamp",
 )
 
 _lock = threading.Lock()
@@ -128,6 +129,8 @@ def lib() -> ctypes.CDLL:
             h.vx_flash_attn_split_plan.restype = _i32
             h.vx_flash_attn_split_plan.argtypes = [_i32] * 6 + [ctypes.POINTER(_i32), ctypes.POINTER(_i32),
                                                                ctypes.POINTER(_i64)]
+            h.vx_debug_clock_stamp.restype = _i32
+            h.vx_debug_clock_stamp.argtypes = [_p, _i32, ctypes.POINTER(_i32), _p]
             h.vx_last_launch.restype = ctypes.c_char_p
             h.vx_last_launch.argtypes = []
             _lib = h
@@ -148,6 +151,19 @@ def flash_plan(batch: int, seq_q: int, seq_k: int, num_heads: int, head_dim: int
     buf = ctypes.create_string_buffer(64)
     raise_for(lib().vx_flash_attn_plan(batch, seq_q, seq_k, num_heads, head_dim, mask_kind, buf, 64))
     return buf.value.decode()
+
+
+_FAKE_PTR = 1 << 20  # a 16-byte aligned address for host-only checks (never dereferenced)
+
+
+def flash_shape_check(batch: int, seq_q: int, seq_k: int, num_heads: int, head_dim: int):
+    """(code, message) of vx_flash_attn_check for contiguous tensors of this
+    shape, without a GPU: VX_OK, or VX_ERR_UNSUPPORTED for a shape the
+    kernels do not take (e.g. a head dim other than 64 or 128)."""
+    rc = lib().vx_flash_attn_check(_FAKE_PTR, _FAKE_PTR, _FAKE_PTR, _FAKE_PTR, None, None, None, 0,
+                                   int(batch), int(seq_q), int(seq_k), int(num_heads), int(head_dim),
+                                   None, None, None, None, ctypes.c_float(1.0))
+    return rc, ("" if rc == VX_OK else last_error())
 
 
 def na3d_plan(t: int, h: int, w: int, head_dim: int, kernel_t: int, kernel_h: int, kernel_w: int) -> str:

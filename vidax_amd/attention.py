@@ -21,6 +21,7 @@ from . import _lib
 __all__ = [
     "flash_attention",
     "flash_kernel_name",
+    "flash_supported",
     "local_attention",
     "dot_product_attention",
     "masked_self_attention",
@@ -106,6 +107,28 @@ def _full_bias(bias, B: int, H: int, Sq: int, Sk: int, dev) -> Tuple[torch.Tenso
     return x, strides
 
 
+def flash_supported(batch: int, seq_q: int, seq_k: int, num_heads: int, head_dim: int) -> bool:
+    """Whether the flash kernels take q (batch, seq_q, num_heads, head_dim)
+    against keys of seq_k: a host-only check (the C ABI's
+    vx_flash_attn_check), so a caller can decide at trace time. The kernels
+    take head dims 64 and 128; the reference's own dispatcher keeps
+    `jax.nn.dot_product_attention` for shapes its kernel cannot take
+    (`src/vidax/core/attention.py:519-533`), e.g. CLIP's D=80
+    (`wan/wan2_1/clip_vision.py:36-46`) and the Wan VAE's single D=384 head
+    (`wan/common/vae_layers.py:100-110`), and a drop-in branch does the same."""
+    return _lib.flash_shape_check(batch, seq_q, seq_k, num_heads, head_dim)[0] == _lib.VX_OK
+
+
+def _require_supported(B: int, Sq: int, Sk: int, H: int, D: int) -> None:
+    rc, msg = _lib.flash_shape_check(B, Sq, Sk, H, D)
+    if rc == _lib.VX_ERR_UNSUPPORTED:
+        raise NotImplementedError(
+            f"vidax_amd: {msg}. This shape is outside the gfx950 flash kernels; the reference keeps "
+            "jax.nn.dot_product_attention for it (src/vidax/core/attention.py:533), and a drop-in "
+            "integration branches on vidax_amd.flash_supported(...) before calling these entry points")
+    _lib.raise_for(rc)
+
+
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                     scale: Optional[float] = None,
                     kv_len: Optional[torch.Tensor] = None,
@@ -130,6 +153,7 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     _check_qkv(q, k, v)
     B, Sq, H, D = q.shape
     Sk = k.shape[1]
+    _require_supported(B, Sq, Sk, H, D)
     if scale is None:
         scale = D ** -0.5
     scale = float(scale)
@@ -172,7 +196,8 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         # grids whose last round would leave the device mostly idle split
         # that round's query tiles over two key halves (fp32 partials in a
         # workspace from torch's caching allocator)
-        ws_bytes = int(L.vx_flash_attn_workspace_size(B, Sq, Sk, H, D))
+        # (calls with a key bias never split: no workspace)
+        ws_bytes = 0 if key_bias_t is not None else int(L.vx_flash_attn_workspace_size(B, Sq, Sk, H, D))
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
         rc = L.vx_flash_attn_ws_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
@@ -189,11 +214,27 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
 
 
 def flash_kernel_name(batch: int, seq_q: int, seq_k: int, num_heads: int, head_dim: int = 128,
-                      mask_kind: int = 0) -> str:
+                      mask_kind: int = 0, num_cus: Optional[int] = None) -> str:
     """Name of the kernel the library launches for this shape (the C ABI's
     launch plan: the gfx950 tile table or VIDAX_FLASH_BLOCK_SIZES). mask_kind:
-    1 key validity, 2 key bias, 4 full bias (bits)."""
-    return _lib.flash_plan(int(batch), int(seq_q), int(seq_k), int(num_heads), int(head_dim), int(mask_kind))
+    1 key validity, 2 key bias, 4 full bias (bits).
+
+    Without num_cus: the kernel of vx_flash_attn_fwd, which never splits its
+    keys. With num_cus (the device's compute units): the kernel of
+    vx_flash_attn_ws_fwd given its workspace, as flash_attention calls it,
+    i.e. flash_fwd_split_kernel<...> for the grids whose last round the key
+    split evens out (vx_flash_attn_split_plan; never with a key or full bias)."""
+    name = _lib.flash_plan(int(batch), int(seq_q), int(seq_k), int(num_heads), int(head_dim), int(mask_kind))
+    if num_cus is not None and int(mask_kind) in (0, 1) and name.startswith("flash_fwd_kernel<"):
+        items = ctypes.c_int32(0)
+        key = ctypes.c_int32(0)
+        nbytes = ctypes.c_int64(0)
+        _lib.raise_for(_lib.lib().vx_flash_attn_split_plan(int(batch), int(seq_q), int(seq_k), int(num_heads),
+                                                           int(head_dim), int(num_cus), ctypes.byref(items),
+                                                           ctypes.byref(key), ctypes.byref(nbytes)))
+        if items.value > 0:
+            name = name.replace("flash_fwd_kernel<", "flash_fwd_split_kernel<")
+    return name
 
 
 def _single_device(mesh) -> None:
@@ -233,40 +274,6 @@ def local_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return flash_attention(q, k, v, scale=sm_scale)
 
 
-# Calls of at least this many (batch, head, query, key) pairs look at their
-# key-only masks on the host first (a few device reductions and one
-# synchronisation: tens of microseconds against a kernel of milliseconds)
-# and hand the kernel the cheapest equivalent form: a key bias of only 0 and
-# -inf (Cosmos3's padding bias, cosmos3/dit_layers.py:124-130) becomes a
-# validity mask, and a validity mask whose valid keys are a prefix of each
-# batch item's keys (HunyuanVideo's joint attention) becomes kv_len alone.
-# The key-bias kernel ran ~14 % and the validity kernel ~4 % slower than the
-# unmasked one at these sizes. Skipped while the stream is being captured
-# into a graph.
-_PREFIX_CHECK_MIN_PAIRS = 1 << 34
-
-
-def _cheaper_key_masks(pairs: int, key_valid: Optional[torch.Tensor], key_bias: Optional[torch.Tensor],
-                       kv_len: Optional[torch.Tensor]):
-    """(key_valid, key_bias) in the cheapest form with the same meaning,
-    given kv_len (the last valid key + 1 of the combined masks)."""
-    if (key_valid is None and key_bias is None) or pairs < _PREFIX_CHECK_MIN_PAIRS or \
-            torch.cuda.is_current_stream_capturing():
-        return key_valid, key_bias
-    valid = key_valid
-    checks = []
-    if key_bias is not None:
-        bias_valid = key_bias == 0
-        checks.append((bias_valid | (key_bias == float("-inf"))).all())
-        valid = bias_valid if valid is None else (valid & bias_valid)
-    # (with kv_len from the combined masks: count of valid keys == last valid index + 1)
-    checks.append((valid.sum(dim=-1, dtype=torch.int32) == kv_len).all())
-    flags = torch.stack(checks).tolist()
-    if key_bias is not None and not flags[0]:
-        return key_valid, key_bias  # a bias with finite nonzero values
-    return (None if flags[-1] else valid), None
-
-
 def dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           bias: Optional[torch.Tensor] = None,
                           mask: Optional[torch.Tensor] = None,
@@ -277,8 +284,9 @@ def dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     `bias` and `mask` are broadcastable to (B, H, Sq, Sk), as in the
     reference. Key-only forms -- shape (B or 1, 1, 1, Sk), e.g. Cosmos3's
     (B, 1, 1, Sk) -inf padding bias -- run in the flash kernel's key-mask
-    path (the key loop is bounded by the last valid key; large calls get the
-    cheapest equivalent form, _cheaper_key_masks). Head- or
+    path: the key loop is bounded by the last valid key, and the kernel
+    classifies each 64-key tile itself (all-zero bias, all-valid tiles run
+    unmasked), so no mask is inspected on the host. Head- or
     query-dependent ones -- T5's relative-position bias, causal masks, the
     reference's `jax.nn.dot_product_attention` fallback -- run in the same
     kernel with a per-(query, key) bias (a boolean mask becomes 0 / -inf).
@@ -287,6 +295,7 @@ def dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     _single_device(mesh)
     B, Sq, H, D = q.shape
     Sk = k.shape[1]
+    _require_supported(B, Sq, Sk, H, D)
     sm_scale = D ** -0.5 if scale is None else scale
     key_bias = key_valid = kv_len = full = None
     valid = None
@@ -308,8 +317,6 @@ def dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             valid = key_valid if valid is None else (valid & key_valid)
     if valid is not None:
         kv_len = _last_valid_plus_one(valid)
-        if full is None:
-            key_valid, key_bias = _cheaper_key_masks(B * H * Sq * Sk, key_valid, key_bias, kv_len)
     return flash_attention(q, k, v, scale=sm_scale, kv_len=kv_len, key_valid=key_valid,
                            key_bias=key_bias, bias=full)
 
@@ -323,9 +330,10 @@ def masked_self_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     key_valid (B, S) bool/int marks valid keys; every query row (valid or
     not) attends exactly the valid keys, as the reference's segment ids do
     (q ids all 1, kv ids = key_valid; `dit_layers.py:183-186`). The reference
-    documents valid keys as a prefix; any pattern is handled exactly here,
-    and the key loop stops at the last valid key. Large calls whose mask is
-    a prefix run with kv_len alone (_cheaper_key_masks).
+    documents valid keys as a prefix; any pattern is handled exactly here:
+    the key loop stops at the last valid key, and tiles whose keys are all
+    valid run the unmasked path (classified by the kernel, with no host
+    synchronisation).
     """
     del tp_sharded  # selects a shard_map wrapper in the reference; one GPU here
     _check_qkv(q, k, v)
@@ -337,6 +345,5 @@ def masked_self_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     else:
         kv = torch.as_tensor(key_valid, device=q.device).reshape(b, k.shape[1]).to(torch.bool)
         kv_len = _last_valid_plus_one(kv)
-        kv, _ = _cheaper_key_masks(b * h * s * k.shape[1], kv, None, kv_len)
         out = flash_attention(q, k, v, scale=scale, kv_len=kv_len, key_valid=kv)
     return out.reshape(b, s, h * d)

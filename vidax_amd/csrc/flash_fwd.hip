@@ -34,6 +34,7 @@
 #include "vx_kernels.h"
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -233,9 +234,23 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
   // the scaled logit plus bias * log2(e) and bias tiles stay on the fast path.
   // With a per-(query, key) bias every tile takes the masked path anyway, and
   // the key bias is added there, next to the full bias (fewer registers).
+  //
+  // Key-mask tiles are classified on the device from the words staged in the
+  // tile's mask slot, lane l holding word l of the tile and one ballot giving
+  // the class: a tile whose 64 biases are all zero starts its accumulators at
+  // zero (no bias reads or scaling), and a tile whose 64 validity bytes are
+  // all set takes the unmasked softmax. So a key mask costs little on the
+  // tiles it leaves unmasked (a padding run of -inf, or a validity hole,
+  // touches few tiles), without the caller inspecting it on the host.
   const float inv_scale = 1.0f / a.scale;
-  auto acc_init = [&](int j, f32x16 (&S)[2]) {
-    if ((MASK & kMaskBias) && !kFull) {
+  auto bias_word = [&](int j) -> float {
+    return *(const VX_LDS float*)(lds + kMaskBuf + (j & (kMaskRing - 1)) * kMaskSlot + 64 + lane * 4);
+  };
+  auto valid_byte = [&](int j) -> uint32_t { return lds[kMaskBuf + (j & (kMaskRing - 1)) * kMaskSlot + lane]; };
+  constexpr bool kKeyBiasStart = (MASK & kMaskBias) && !kFull;   // key bias through the accumulator start
+  constexpr bool kValidClass = (MASK & kMaskValid) && !kFull;    // (a full bias masks every tile anyway)
+  auto acc_init = [&](int j, f32x16 (&S)[2], bool nonzero) {
+    if (kKeyBiasStart && nonzero) {
       const lds_u8* bslot = lds + kMaskBuf + (j & (kMaskRing - 1)) * kMaskSlot + 64;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -251,7 +266,7 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
     }
   };
   auto qk = [&](int tile, int buf_off, f32x16 (&S)[2]) {
-    acc_init(tile, S);
+    acc_init(tile, S, kKeyBiasStart && __builtin_amdgcn_ballot_w64(bias_word(tile) != 0.f) != 0);
     const lds_u8* kb0 = lds + buf_off;
 #pragma unroll
     for (int ds = 0; ds < kDS; ++ds) {
@@ -374,6 +389,8 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
 
     int kb_cur = 1;         // K buffer holding K_{t+1}  (= (t+1) % kNB)
     int vb_prev = kNB - 1;  // V buffer holding V_{t-1}  (= (t+kNB-1) % kNB)
+    // the current tile has an invalid key (each step classifies the next one)
+    bool invalid_cur = kValidClass && __builtin_amdgcn_ballot_w64(valid_byte(t_begin) == 0) != 0;
     // One key tile: consumes S (scores of tile t) and Pp (probabilities of
     // tile t-1), produces Sn (scores of tile t+1) and P (probabilities of
     // tile t). The loop below calls it twice per trip with the two register
@@ -390,20 +407,26 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
       // iteration's copies.
       wait_prev();
       __syncthreads();
+      // the class words of tile t+1 (its mask slot landed with K_{t+1}),
+      // read first so that their latency is covered by the work below: its
+      // validity class is taken at the end of this step (for the next one),
+      // its bias class before its accumulator start
+      float bias_next = 0.f;
+      uint32_t valid_next = 1;
+      if (kKeyBiasStart) bias_next = bias_word(t + 1);
+      if (kValidClass) valid_next = valid_byte(t + 1);
       const int kb_next = kb_cur == 0 ? kNB - 1 : kb_cur - 1;     // t % kNB
       const int vb_next = vb_prev == 0 ? kNB - 1 : vb_prev - 1;  // (t+kNB-2) % kNB
 
       // ---- key masks. Tiles that hold a masked key (the tail tile, a
-      // key_valid hole, any key_bias) take the scores to log2 units here,
-      // masked keys -> -inf, and use cc = 1 below; fully valid tiles keep the
-      // fused scale in the exp argument.
+      // key_valid hole) take the scores to log2 units here, masked keys ->
+      // -inf, and use cc = 1 below; fully valid tiles (and key bias tiles,
+      // whose bias is in the accumulator start) keep the fused scale in the
+      // exp argument.
       const int key0 = t * kBN;
       const lds_u8* mslot = lds + kMaskBuf + (t & (kMaskRing - 1)) * kMaskSlot;  // tile t's mask
       bool slow = key0 + kBN > kv_end;
-      if (MASK & kMaskValid) {
-        // lane l tests validity byte l of the tile: one LDS byte per lane
-        slow = slow || __builtin_amdgcn_ballot_w64(mslot[lane] == 0) != 0;
-      }
+      if (kValidClass) slow = slow || invalid_cur;  // tile t has an invalid key (classified last step)
       if (MASK & kMaskFull) slow = true;
       // this iteration's copies: K_{t+kNB}, its mask and V_{t+kNB-2}
       if (COPY) {
@@ -504,7 +527,8 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
           __builtin_amdgcn_sched_barrier(0);
         };
         if (WAVES == 4 || COPY) softmax_block();
-        acc_init(t + 1, Sn);  // read by the QK^T slots (16 and on)
+        // read by the QK^T slots (16 and on)
+        acc_init(t + 1, Sn, kKeyBiasStart && __builtin_amdgcn_ballot_w64(bias_next != 0.f) != 0);
 #pragma unroll
         for (int s = 0; s < kSlots; ++s) {
           if (s + 3 < kSlots) fr[s + 3] = frag(s + 3);
@@ -550,6 +574,7 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
       l_run += l_tile;
       kb_cur = kb_cur == kNB - 1 ? 0 : kb_cur + 1;
       vb_prev = vb_prev == kNB - 1 ? 0 : vb_prev + 1;
+      if (kValidClass) invalid_cur = __builtin_amdgcn_ballot_w64(valid_next == 0) != 0;
     };
 
     f32x16 S2[2];
@@ -928,24 +953,39 @@ void flash_stream_kernel(const FlashArgs a) {
 
   // output rows of table entry e, normalised by the row sum l (one 32-wide
   // d block at a time: few registers, as it runs inside the key loop).
-  // Lanes past Sq hold row Sq-1's query (the q copies repeat that row), so
-  // they store row Sq-1's output again, the same bytes: every wave issues
-  // exactly 2 * kDB stores, which the copying waves' waits count.
+  // Every wave issues exactly 2 * kDB store instructions, which the copying
+  // waves' waits count, so a wave never skips one. Lanes past Sq hold row
+  // Sq-1's query (the q copies repeat that row) but must not store it: their
+  // probabilities may round differently from the owner's (the rare rescale
+  // is taken per wave). The stores go through a buffer resource that ends at
+  // the item's last row below Sq, and those lanes' offsets lie past its end,
+  // where the hardware drops the write (the instruction still counts).
+  const uint64_t o_addr = uniform_u64((uint64_t)(uintptr_t)a.o);
   auto epilogue = [&](int e, float l) __attribute__((always_inline)) {
     const float lt = halves_sum(l);
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     const Item it = entry(e);
     int ln_ = lane;
     asm volatile("" : "+v"(ln_));
-    const int qi = (it.qt * kWaves + wave) * 32 + (ln_ & 31);
-    bf16* orow = (bf16*)a.o + (it.b * a.os[0] + it.h * a.os[2]) + (int64_t)min(qi, a.Sq - 1) * a.os[1];
+    const int r0 = it.qt * 256;                   // the item's first query row
+    const int rows = uni(min(256, a.Sq - r0));    // its rows below Sq
+    const int qloc = wave * 32 + (ln_ & 31);
+    // (offsets below 2^31: the plan keeps the output's row stride <= 2^22 elements)
+    const uint64_t base =
+        o_addr + (uint64_t)((int64_t)it.b * a.os[0] + (int64_t)it.h * a.os[2] + (int64_t)r0 * a.os[1]) * 2u;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(uintptr_t)base, (short)0, (int)(((int64_t)(rows - 1) * a.os[1] + D) * 2), 0x00020000);
+    const uint32_t row_off = qloc < rows ? (uint32_t)(qloc * (int)a.os[1]) * 2u : 0x80000000u;
 #pragma unroll
     for (int db = 0; db < kDB; ++db) {
       u32x4 chunk[1][2];
       const f32x16 Ob[1] = {O[db]};
       pack_out_rows<1>(Ob, inv, chunk);
 #pragma unroll
-      for (int pr = 0; pr < 2; ++pr) *(u32x4*)(orow + db * 32 + (2 * pr + (ln_ >> 5)) * 8) = chunk[0][pr];
+      for (int pr = 0; pr < 2; ++pr)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, chunk[0][pr]), rs,
+                                               row_off + (uint32_t)(db * 32 + (2 * pr + (ln_ >> 5)) * 8) * 2u, 0,
+                                               0);
     }
   };
   auto probs = [&](const f32x16 (&S)[2], float cc_, float m, bf16x8 (&P)[2][2]) __attribute__((always_inline)) -> float {
@@ -1372,15 +1412,17 @@ int noalloc_scratch(void** ptr, int64_t* bytes) {
 }
 
 int device_cu_count() {
-  static int counts[64] = {0};
+  // per-device cache; host threads may race to fill an entry, each storing
+  // the same value (relaxed atomics: no data race)
+  static std::atomic<int> counts[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (counts[dev] == 0) {
-    int n = 0;
+  int n = counts[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    counts[dev] = n;
+    counts[dev].store(n, std::memory_order_relaxed);
   }
-  return counts[dev];
+  return n;
 }
 
 int launch_flash_fwd(const FlashArgs& a, void* stream, const char** launched) {

@@ -307,8 +307,9 @@ int32_t flash_check(const void* q, const void* k, const void* v, const void* out
   const int32_t mask_kind =
       (key_valid != nullptr ? 1 : 0) | (key_bias != nullptr ? 2 : 0) | (full_bias != nullptr ? 4 : 0);
   if ((rc = flash_plan(B, Sq, Sk, H, mask_kind, &waves, &stream)) != VX_OK) return rc;
-  // the persistent kernel copies q tiles with 32-bit row offsets too
-  if (qs[1] > (int64_t(1) << 24)) stream = 0;
+  // the persistent kernel copies q tiles with 32-bit row offsets too, and
+  // stores each 256-row block of the output through a buffer resource
+  if (qs[1] > (int64_t(1) << 24) || os[1] > (int64_t(1) << 22)) stream = 0;
   if (args != nullptr) {
     args->waves = waves;
     args->stream = stream;
@@ -500,11 +501,23 @@ int32_t injected() {
 
 extern "C" {
 
-int32_t vx_abi_version(void) { return 10600; }
+int32_t vx_abi_version(void) { return 10700; }
 
 const char* vx_last_error(void) { return g_error; }
 
 void vx_debug_inject_error(int32_t code) { g_inject.store(code, std::memory_order_relaxed); }
+
+int32_t vx_debug_clock_stamp(uint64_t* out, int32_t n_groups, int32_t* wall_clock_khz, void* stream) {
+  if (out == nullptr || wall_clock_khz == nullptr)
+    return fail(VX_ERR_INVALID_ARGUMENT, "out and wall_clock_khz must be non-NULL");
+  if ((reinterpret_cast<uintptr_t>(out) & 7u) != 0) return fail(VX_ERR_INVALID_ARGUMENT, "out must be 8-byte aligned");
+  if (n_groups < 1 || n_groups > 4096) return fail(VX_ERR_INVALID_ARGUMENT, "n_groups must be in 1..4096");
+  int khz = 0;
+  const int err = vx::launch_clock_stamp(out, n_groups, stream, &khz);
+  if (err != 0) return fail(VX_ERR_LAUNCH, "clock stamp launch failed (hipError_t %d)", err);
+  *wall_clock_khz = khz;
+  return ok();
+}
 
 const char* vx_last_launch(void) { return g_last_launch; }
 

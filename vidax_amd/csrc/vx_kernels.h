@@ -113,4 +113,9 @@ int launch_flash_fwd(const FlashArgs& a, void* stream, const char** launched);
 int launch_na3d_fwd(const Na3dArgs& a, void* stream, const char** launched);
 int launch_qk_prologue(const PrologueArgs& a, void* stream, const char** launched);
 
+// Measurement only: n_groups one-wave workgroups each store (XCD id, HW_ID,
+// shader clock counter, real-time counter) as four uint64 at out + 4 * group;
+// *wall_clock_khz receives the real-time counter's rate.
+int launch_clock_stamp(uint64_t* out, int n_groups, void* stream, int* wall_clock_khz);
+
 }  // namespace vx
