@@ -410,7 +410,20 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   // key rows in that XCD's L2.
   const int n_bricks = a.T * n_yb * n_xb;
   int brick, head;
-  if ((a.NH & 7) == 0) {
+  if (a.order == kNaOrderTColumns) {
+    // Deep t windows: XCD x takes the x-th eighth of the (head, brick
+    // column (y, x), t) sequence, t fastest, so its resident workgroups hold
+    // bricks of consecutive t planes of one column, which share kt' - 1 of
+    // their kt' key planes in that XCD's L2.
+    const int total = n_bricks * a.NH;
+    const int lin = blockIdx.y * n_bricks + blockIdx.x;  // launch order within a batch item
+    const int xcd = lin & 7, j = lin >> 3;
+    const int g = xcd * (total >> 3) + min(xcd, total & 7) + j;  // the eighths are contiguous ranges of g
+    const int ncol = n_yb * n_xb;
+    const int rest = g / a.T;
+    head = rest / ncol;
+    brick = (g - rest * a.T) * ncol + (rest - head * ncol);     // (t * n_yb + yb) * n_xb + xb
+  } else if ((a.NH & 7) == 0) {
     const int lin = blockIdx.y * n_bricks + blockIdx.x;  // launch order within a batch item
     const int xcd = lin & 7, j = lin >> 3;
     head = xcd + 8 * (j / n_bricks);

@@ -384,6 +384,7 @@ int32_t na3d_check(const void* q, const void* k, const void* v, const void* out,
     args->kw = kw < W ? kw : W;
     args->scale = scale;
     args->variant = na3d_variant(args->kw, D, Hs, W);
+    args->order = args->kt >= vx::kNaTColumnsMinKt ? vx::kNaOrderTColumns : vx::kNaOrderLaunch;
     args->q_prep = 0;
     args->q_weight = nullptr;
     args->q_cos = args->q_sin = nullptr;

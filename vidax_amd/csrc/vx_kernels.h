@@ -62,6 +62,7 @@ struct Na3dArgs {
   int32_t kt, kh, kw;  // window sizes already clamped to the grid extents
   float scale;
   int32_t variant;     // kernel chosen by the launch plan (Na3dVariant)
+  int32_t order;       // brick order of the pipelined kernels (Na3dOrder), chosen by the launch plan
   // q preparation applied by the kernel as it loads q (0 = q is used as
   // given): bit 1 per-head RMSNorm with q_weight[D] and q_eps, bit 2 times
   // bf16(q_post_scale), bit 4 rotation of adjacent pairs by the token's
@@ -85,6 +86,15 @@ enum Na3dVariant : int32_t {
   kNaWave = 3,    // 25 < kw' <= 57, head dim 128: per-wave bricks
   kNaTallWide = 4,  // head dim 64, 9 < kw' <= 13, round_up(W, 32) == round_up(W, 16): 1 x 8 x 32 bricks
 };
+
+// Order in which the pipelined NA kernels' workgroups take their bricks.
+enum Na3dOrder : int32_t {
+  kNaOrderLaunch = 0,    // launch order (heads spread over the XCDs when NH % 8 == 0)
+  kNaOrderTColumns = 1,  // each XCD walks consecutive t planes of brick columns (deep t windows)
+};
+// t windows (clamped) from which the plan picks kNaOrderTColumns: bricks of
+// consecutive t planes then share kt' - 1 of their kt' key planes in an L2
+constexpr int32_t kNaTColumnsMinKt = 5;
 
 struct PrologueArgs {
   const void* x;        // bf16 rows of H * D
