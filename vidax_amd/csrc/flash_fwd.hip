@@ -1037,20 +1037,28 @@ void flash_stream_kernel(const FlashArgs a) {
   };
   wait_prev();
   __syncthreads();
-  load_q(qr);
-  f32x16 S[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-  for (int ds = 0; ds < kDS; ++ds)
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const bf16x8 kf = *(const VX_LDS bf16x8*)(lds + kKBuf + kofs(ds & 3) + kb * 32 * 128 + (ds >> 2) * C::kHalfBytes);
-      S[kb] = mfma32x32x16(kf, qr[ds], S[kb]);
-    }
+  // q of the first item and the scores of its first tile, formed at the top
+  // of each wave kind's loop (below): formed before the branch into the two
+  // loops, q was spilled across it
+  f32x16 S[2];
   bf16x8 Pp[2][2];
+  auto first_scores = [&]() __attribute__((always_inline)) {
+    load_q(qr);
+    S[0] = f32x16{};
+    S[1] = f32x16{};
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
+    for (int ds = 0; ds < kDS; ++ds)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) Pp[kb][j] = bf16x8{};
+      for (int kb = 0; kb < 2; ++kb) {
+        const bf16x8 kf =
+            *(const VX_LDS bf16x8*)(lds + kKBuf + kofs(ds & 3) + kb * 32 * 128 + (ds >> 2) * C::kHalfBytes);
+        S[kb] = mfma32x32x16(kf, qr[ds], S[kb]);
+      }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) Pp[kb][j] = bf16x8{};
+  };
 
   int kb_cur = 1;   // K buffer holding K_{u+1}
   int vb_prev = 1;  // V buffer holding V_{u-1}
@@ -1262,6 +1270,7 @@ void flash_stream_kernel(const FlashArgs a) {
   f32x16 S2[2];
   bf16x8 P2[2][2];
   auto stream_loop = [&](auto copy_tag) __attribute__((always_inline)) {
+    first_scores();
     int u = 0;
     for (; u + 1 < U; u += 2) {
       stream_step(copy_tag, u, S, S2, Pp, P2);

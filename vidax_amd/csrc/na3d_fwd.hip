@@ -570,13 +570,20 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     if (C::kRows == 2) advance(c);
     return rr;
   };
-  // Issues one tensor's copies of one step's rows.
+  // Issues one tensor's copies of one step's rows. When a step's copies do
+  // not divide evenly over the waves, the waves below kExtraWaves issue one
+  // more. (Making that a compile-time tag of the key loop, as IN below is,
+  // made the 8-wave tall kernel spill.)
+  constexpr int kExtraWaves = C::kCopies % C::kWaves;
+  const bool extra = kExtraWaves == 0 || wave < kExtraWaves;  // wave-uniform
   auto issue = [&](const bf16* base, int slot_off, const StepRows& rr) {
 #pragma unroll
     for (int p = 0; p < C::kCopiesPerWave; ++p)
-      if (C::kCopies % C::kWaves == 0 || wave + C::kWaves * p < C::kCopies)
+      if (kExtraWaves == 0 || p + 1 < C::kCopiesPerWave || extra)
         lds_dma16_buf(raw_rsrc(base + (dma_row[p] ? rr.tok1 : rr.tok0)), dma_voff[p], lds_base + slot_off + dma_dst[p]);
   };
+  using True = std::integral_constant<bool, true>;
+  using False = std::integral_constant<bool, false>;
 
   // ---- per-lane LDS offsets (half-plane 0; d 64-127 add kHalfL). K
   // fragment: key col of the chunk (SEG = 16: keys 0-15 from the step's first
@@ -645,8 +652,11 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   // One step: consumes S (scores of chunk s) and Pp (probabilities of chunk
   // s-1), produces Sn (scores of chunk s+1) and P (probabilities of chunk s).
   // rr: the rows of step s on entry (their K was issued two steps ago), the
-  // rows of step s + 2 on return.
-  auto step = [&](const int s, f32x16& S, f32x16& Sn, const bf16x8 (&Pp)[2], bf16x8 (&P)[2], StepRows& rr) {
+  // rows of step s + 2 on return. IN (compile-time, so that the loop carries
+  // no per-step test of it): some query of this wave lies inside the grid.
+  auto step = [&](auto in_tag, const int s, f32x16& S, f32x16& Sn, const bf16x8 (&Pp)[2], bf16x8 (&P)[2],
+                  StepRows& rr) __attribute__((always_inline)) {
+    constexpr bool IN = decltype(in_tag)::value;
     // The previous step's copies (K of s+1, V of s-1) have landed once this
     // wave has none outstanding; the barrier publishes everyone's and frees
     // K slot s%2 (K of s, read last step) and V slot s%2 (V of s-2).
@@ -667,7 +677,10 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 
     const VX_LDS unsigned char* kb = lds + C::kK + ((s + 1) & 1) * C::kSlot;  // K of chunk s+1
     const VX_LDS unsigned char* vb = lds + C::kV + ((s + 1) & 1) * C::kSlot;  // V of chunk s-1
-    if (!wave_in) {
+    // (IN is the tag's value; the 1 x 4 x 32 bricks pass the runtime flag
+    // instead, one loop for all waves: their two loops measured ~1 % slower
+    // at the (3,7,7) config, whose x edge holds waves without queries)
+    if (!(IN && (TALL || wave_in))) {
       // no query of this wave is inside the grid (the ragged x or y edge):
       // it only copies its share of the rows
       P[0] = bf16x8{};
@@ -809,16 +822,24 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 
   f32x16 S2;
   bf16x8 P2[2];
-  int s = 0;
-  for (; s + 1 < n_steps; s += 2) {
-    step(s, S, S2, Pp, P2, rows_even);
-    step(s + 1, S2, S, P2, Pp, rows_odd);
-  }
-  if (s < n_steps) {
-    step(s, S, S2, Pp, P2, rows_even);
-    Pp[0] = P2[0];
-    Pp[1] = P2[1];
-  }
+  // the key loop; the tall bricks run one copy for the waves with queries
+  // and one for the others
+  auto key_loop = [&](auto in_tag) __attribute__((always_inline)) {
+    int s = 0;
+    for (; s + 1 < n_steps; s += 2) {
+      step(in_tag, s, S, S2, Pp, P2, rows_even);
+      step(in_tag, s + 1, S2, S, P2, Pp, rows_odd);
+    }
+    if (s < n_steps) {
+      step(in_tag, s, S, S2, Pp, P2, rows_even);
+      Pp[0] = P2[0];
+      Pp[1] = P2[1];
+    }
+  };
+  if (!TALL || wave_in)
+    key_loop(True{});
+  else
+    key_loop(False{});
   // ---- PV of the last chunk (its V was issued by the last step).
   wait_vmem<0>();
   __syncthreads();
