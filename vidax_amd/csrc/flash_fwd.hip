@@ -838,17 +838,9 @@ void flash_stream_kernel(const FlashArgs a) {
   // ---- LDS offsets (the layout of flash_tile: half-planes of 64 rows x
   // 128 bytes, 16-byte chunks XOR-swizzled per row)
   // K fragment (kb, ds): key kb*32 + col, chunk 2*(ds%4) + hf of half ds/4,
-  // at koff0 ^ ((ds % 4) << 5) (2*(ds%4) + hf = 2*(ds%4) ^ hf). The q
-  // reloads inside the key loop form their offsets at each use from a value
-  // made opaque by an empty asm, so that those do not hold registers across
-  // the whole loop, which has none to spare.
+  // at koff0 ^ ((ds % 4) << 5) (2*(ds%4) + hf = 2*(ds%4) ^ hf).
   const int koff0 = col * 128 + ((hf ^ half_swizzle(col)) * 16);
   auto kofs = [&](int d4) { return koff0 ^ (d4 << 5); };
-  auto kofs_loop = [&](int d4) __attribute__((always_inline)) {
-    int k = koff0;
-    asm volatile("" : "+v"(k));
-    return k ^ (d4 << 5);
-  };
   const int i16 = lane & 15;
   const int vr = i16 >> 2, vc4 = i16 & 3, dh = (lane >> 4) & 1;
   int voff[2];
@@ -865,14 +857,13 @@ void flash_stream_kernel(const FlashArgs a) {
   const uint64_t v_tile_bytes = uniform_u64((uint64_t)a.vs[1] * (2 * kBN));
   // this wave's copies of 64 rows from byte address `addr` into the LDS tile
   // at buf_off; rows from rows_left on repeat row rows_left - 1 (>= 0)
-  // (the per-lane offsets are formed at each call: an empty asm on the lane
-  // index keeps them out of the registers of the whole key loop)
+  // (the per-lane offsets of whole tiles are loop-invariant, held in
+  // registers: forming them at each call, to keep registers free, cost 3 %
+  // at 32760 x 512 keys)
   auto stage_clamped = [&](uint64_t addr, int64_t stride, int rows_left, int buf_off) __attribute__((always_inline)) {
     const i32x4_rsrc rs = raw_rsrc_u64(addr);
     const uint32_t dst = lds_base + buf_off + (uint32_t)(wave * kLoadsPerWave) * 1024u;
-    int ln_ = lane;
-    asm volatile("" : "+v"(ln_));
-    const int sr = ln_ >> 3, sc = ln_ & 7;
+    const int sr = lane >> 3, sc = lane & 7;
     if (rows_left >= kBN) {
       // row r = 8*(i%8) + sr: its swizzle depends on sr and on bit 0 of i,
       // the rest of the offset is uniform
@@ -910,7 +901,7 @@ void flash_stream_kernel(const FlashArgs a) {
     const lds_u8* qb = lds + kQBuf + (wave >> 1) * kTileBytes + (wave & 1) * 32 * 128;
 #pragma unroll
     for (int ds = 0; ds < kDS; ++ds)
-      qr[ds] = *(const VX_LDS bf16x8*)(qb + kofs_loop(ds & 3) + (ds >> 2) * C::kHalfBytes);
+      qr[ds] = *(const VX_LDS bf16x8*)(qb + kofs(ds & 3) + (ds >> 2) * C::kHalfBytes);
   };
 
   // ---- copy cursors (wave-uniform): byte address of the tile's first row,
@@ -965,11 +956,9 @@ void flash_stream_kernel(const FlashArgs a) {
     const float lt = halves_sum(l);
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     const Item it = entry(e);
-    int ln_ = lane;
-    asm volatile("" : "+v"(ln_));
     const int r0 = it.qt * 256;                   // the item's first query row
     const int rows = uni(min(256, a.Sq - r0));    // its rows below Sq
-    const int qloc = wave * 32 + (ln_ & 31);
+    const int qloc = wave * 32 + col;
     // (offsets below 2^31: the plan keeps the output's row stride <= 2^22 elements)
     const uint64_t base =
         o_addr + (uint64_t)((int64_t)it.b * a.os[0] + (int64_t)it.h * a.os[2] + (int64_t)r0 * a.os[1]) * 2u;
@@ -984,7 +973,7 @@ void flash_stream_kernel(const FlashArgs a) {
 #pragma unroll
       for (int pr = 0; pr < 2; ++pr)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, chunk[0][pr]), rs,
-                                               row_off + (uint32_t)(db * 32 + (2 * pr + (ln_ >> 5)) * 8) * 2u, 0,
+                                               row_off + (uint32_t)(db * 32 + (2 * pr + hf) * 8) * 2u, 0,
                                                0);
     }
   };
@@ -1087,9 +1076,7 @@ void flash_stream_kernel(const FlashArgs a) {
     float cc_ = c;
     if (slow) {  // the item's tail tile: keys from kv_end on -> -inf
       cc_ = 1.0f;
-      int ln_ = lane;
-      asm volatile("" : "+v"(ln_));
-      const int hf4 = (ln_ >> 5) * 4;
+      const int hf4 = hf * 4;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
