@@ -263,7 +263,9 @@ class _ClockStamps:
     launched on the kernel's stream right before the loop and right after
     it. The shader counter is kept per CU, so the stamps are paired by CU
     (XCD, shader engine, CU): shader cycles passed / real time passed is that
-    CU's clock over the loop; the median over the CUs is reported."""
+    CU's clock over the loop. The XCDs hold different clocks (a spread of
+    ~7 % at full load), so the mean over the CUs is reported: the figure
+    GRBM_GUI_ACTIVE (summed over the 8 XCDs) / 8 / duration gives."""
 
     GROUPS = 1024
 
@@ -463,10 +465,10 @@ def main(argv=None):
     # The shader clock held over the timed loop, and the work per clock cycle
     # at that clock: flop/cycle over PEAK_BF16_FLOP_PER_CYCLE is the
     # matrix-core fraction independent of the clock the box held.
-    roofline["sclk_mhz"] = round(sclk["median"], 1) if sclk else None
+    roofline["sclk_mhz"] = round(sclk["mean"], 1) if sclk else None
     if sclk:
         roofline["sclk"] = {k: (round(v, 1) if isinstance(v, float) else v) for k, v in sclk.items()}
-        cycles = ms * 1e-3 * sclk["median"] * 1e6
+        cycles = ms * 1e-3 * sclk["mean"] * 1e6
         if flops:
             roofline["flop_per_cycle"] = round(flops / cycles, 1)
             roofline["frac_of_peak_at_sclk"] = round(flops / cycles / PEAK_BF16_FLOP_PER_CYCLE, 4)
