@@ -75,13 +75,16 @@ struct FCfg {
   static constexpr int kPV = 2 * 2 * kDB;               // MFMAs of PV per tile
   static constexpr int kQK = 2 * kDS;                   // MFMAs of QK^T per tile
   static constexpr int kSlots = kPV + kQK;              // 32 (16)
-  // key masks: tile j's mask in slot j % kMaskRing; the ring holds the
-  // kNB masks in flight plus the one being read
-  static constexpr int kMaskRing = kNB < 4 ? 4 : 8;
+  // key masks: tile j's mask in slot j % kMaskRing. Masks are staged one
+  // tile further ahead than K (tile t + kNB + 1 in iteration t), so the
+  // ring holds the kNB + 1 masks in flight plus the two being read (tile
+  // t's and tile t + 1's).
+  static constexpr int kMaskRing = 8;
+  static_assert(kNB + 3 <= kMaskRing, "mask ring too small");
 };
 // Key masks of the masked variants go through LDS like K: a ring of slots
 // of 320 bytes (64 validity bytes, then 64 fp32 biases), staged by wave 0
-// together with K_j.
+// with the K copies, one tile ahead of K.
 constexpr int kMaskSlot = 320;
 // Mask kinds (template argument, bits): validity bytes per key, additive bias
 // per key, additive bias per (query, key) of each head (read per query row
@@ -352,16 +355,18 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
   if (n_tiles > t_begin) {
     // Tile j of K lives in K buffer j % kNB and tile j of V in V buffer
     // j % kNB; V buffer kNB-1 stands in for "V_{-1}" (zeros, paired with P = 0
-    // in iteration 0). Iteration t issues K_{t+kNB}, its mask and
-    // V_{t+kNB-2}, into the buffers that the previous iteration finished
-    // reading; the prologue issues the same groups for t = -kNB .. -1, so
-    // that every wait below counts whole groups.
+    // in iteration 0). Iteration t issues K_{t+kNB}, the mask of tile
+    // t+kNB+1 and V_{t+kNB-2}, into the buffers that the previous iteration
+    // finished reading; the prologue issues the first mask and then the same
+    // groups for t = -kNB .. -1, so that every wait below counts whole
+    // groups (the first mask is older than all of them).
     if (wave < kCopyWaves) {
       const Lanes ln = make_lanes();
+      stage_mask(t_begin);  // (masks run one tile ahead of K: the first one on its own)
 #pragma unroll
       for (int j = 0; j < kNB; ++j) {
         stage_k(ln, min(t_begin + j, n_tiles - 1), kKBuf + j * kTileBytes);
-        stage_mask(min(t_begin + j, n_tiles - 1));
+        stage_mask(min(t_begin + j + 1, n_tiles - 1));
         if (j >= 2) stage_v(ln, min(t_begin + j - 2, n_tiles - 1), kVBuf + (j - 2) * kTileBytes);
       }
     }
@@ -391,6 +396,10 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
     int vb_prev = kNB - 1;  // V buffer holding V_{t-1}  (= (t+kNB-1) % kNB)
     // the current tile has an invalid key (each step classifies the next one)
     bool invalid_cur = kValidClass && __builtin_amdgcn_ballot_w64(valid_byte(t_begin) == 0) != 0;
+    // the next tile has a nonzero key bias (each step classifies the tile
+    // after next, whose mask has landed one step before its K)
+    bool bias_nz_next =
+        kKeyBiasStart && __builtin_amdgcn_ballot_w64(bias_word(min(t_begin + 1, n_tiles - 1)) != 0.f) != 0;
     // One key tile: consumes S (scores of tile t) and Pp (probabilities of
     // tile t-1), produces Sn (scores of tile t+1) and P (probabilities of
     // tile t). The loop below calls it twice per trip with the two register
@@ -407,13 +416,13 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
       // iteration's copies.
       wait_prev();
       __syncthreads();
-      // the class words of tile t+1 (its mask slot landed with K_{t+1}),
-      // read first so that their latency is covered by the work below: its
-      // validity class is taken at the end of this step (for the next one),
-      // its bias class before its accumulator start
-      float bias_next = 0.f;
+      // the class words of tile t+1's validity and tile t+2's bias (their
+      // mask slots have landed: masks run a tile ahead of K), read first so
+      // that their latency is covered by the work below; both classes are
+      // taken at the end of this step, for the next one
+      float bias_next2 = 0.f;
       uint32_t valid_next = 1;
-      if (kKeyBiasStart) bias_next = bias_word(t + 1);
+      if (kKeyBiasStart) bias_next2 = bias_word(min(t + 2, n_tiles - 1));
       if (kValidClass) valid_next = valid_byte(t + 1);
       const int kb_next = kb_cur == 0 ? kNB - 1 : kb_cur - 1;     // t % kNB
       const int vb_next = vb_prev == 0 ? kNB - 1 : vb_prev - 1;  // (t+kNB-2) % kNB
@@ -428,10 +437,10 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
       bool slow = key0 + kBN > kv_end;
       if (kValidClass) slow = slow || invalid_cur;  // tile t has an invalid key (classified last step)
       if (MASK & kMaskFull) slow = true;
-      // this iteration's copies: K_{t+kNB}, its mask and V_{t+kNB-2}
+      // this iteration's copies: K_{t+kNB}, the mask of tile t+kNB+1 and V_{t+kNB-2}
       if (COPY) {
         stage_k(ln, min(t + kNB, n_tiles - 1), kKBuf + kb_next * kTileBytes);
-        stage_mask(min(t + kNB, n_tiles - 1));
+        stage_mask(min(t + kNB + 1, n_tiles - 1));
         stage_v(ln, min(t + kNB - 2, n_tiles - 1), kVBuf + vb_next * kTileBytes);
       }
       float cc = c;
@@ -528,7 +537,7 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
         };
         if (WAVES == 4 || COPY) softmax_block();
         // read by the QK^T slots (16 and on)
-        acc_init(t + 1, Sn, kKeyBiasStart && __builtin_amdgcn_ballot_w64(bias_next != 0.f) != 0);
+        acc_init(t + 1, Sn, bias_nz_next);
 #pragma unroll
         for (int s = 0; s < kSlots; ++s) {
           if (s + 3 < kSlots) fr[s + 3] = frag(s + 3);
@@ -575,6 +584,7 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
       kb_cur = kb_cur == kNB - 1 ? 0 : kb_cur + 1;
       vb_prev = vb_prev == kNB - 1 ? 0 : vb_prev + 1;
       if (kValidClass) invalid_cur = __builtin_amdgcn_ballot_w64(valid_next == 0) != 0;
+      if (kKeyBiasStart) bias_nz_next = __builtin_amdgcn_ballot_w64(bias_next2 != 0.f) != 0;
     };
 
     f32x16 S2[2];
