@@ -98,6 +98,30 @@ constexpr float kNegBig = -1.0e30f;           // finite "no key seen yet" max
 typedef VX_LDS unsigned char lds_u8;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
+// Stores a wave's 32 output rows (query rows q0 .. q0 + 31 of the head's
+// output, rows at or past Sq dropped): the O^T accumulators normalised by
+// inv and packed (pack_out_rows), one 64-wide d pair at a time (few
+// registers), as whole 128-byte lines (line_chunks).
+template <int kDB>
+__device__ __forceinline__ void store_out_lines(const f32x16 (&O)[kDB], float inv, bf16* obase, int q0, int Sq,
+                                                int64_t os1, int lane) {
+  const int r8 = lane & 7;
+#pragma unroll
+  for (int p = 0; p < kDB / 2; ++p) {
+    u32x4 c2[2][2];
+    const f32x16 Ob[2] = {O[2 * p], O[2 * p + 1]};
+    pack_out_rows<2>(Ob, inv, c2);  // all lanes: cross-lane exchanges
+    u32x4 out[4];
+    line_chunks(c2, out);
+    const uint32_t cofs = line_chunk_offset(lane, p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = q0 + r8 + 8 * i;
+      if (q < Sq) *(u32x4*)((unsigned char*)(obase + (int64_t)q * os1) + cofs) = out[i];
+    }
+  }
+}
+
 // One workgroup's work: query tile `qtile` of (head, b) over the keys
 // [k_lo, k_hi) (k_lo a multiple of the key tile). part < 0 writes the
 // normalised bf16 output rows; part >= 0 writes the unnormalised fp32
@@ -631,21 +655,12 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
     return;
   }
 
-  // ---- epilogue: normalise, pack to 16-byte chunks of 8 consecutive d
-  // (pack_out_rows) and store.
+  // ---- epilogue: normalise, pack to 16-byte chunks of 8 consecutive d,
+  // regroup into whole lines and store.
   const float lt = halves_sum(l_run);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-  const int qi = qw0 + col;
-  u32x4 chunk[kDB][2];
-  pack_out_rows<kDB>(O, inv, chunk);  // all lanes: cross-lane exchange
-  if (qi < a.Sq) {
-    // (the row address is formed here, so nothing of it is live in the key loop)
-    bf16* orow = (bf16*)a.o + (b * a.os[0] + head * a.os[2]) + (int64_t)qi * a.os[1];
-#pragma unroll
-    for (int db = 0; db < kDB; ++db)
-#pragma unroll
-      for (int pr = 0; pr < 2; ++pr) *(u32x4*)(orow + db * 32 + (2 * pr + hf) * 8) = chunk[db][pr];
-  }
+  // (the output address is formed here, so nothing of it is live in the key loop)
+  store_out_lines<kDB>(O, inv, (bf16*)a.o + (b * a.os[0] + head * a.os[2]), qw0, a.Sq, a.os[1], lane);
 }
 
 template <int MASK, int D, int WAVES>
@@ -704,16 +719,8 @@ __global__ __launch_bounds__(WAVES * 64) void flash_combine_kernel(const FlashAr
 #pragma unroll
       for (int e = 0; e < 4; ++e) O[db][4 * k4 + e] = x0[e] * a0 + x1[e] * a1;
     }
-  u32x4 chunk[kDB][2];
-  pack_out_rows<kDB>(O, inv, chunk);
-  const int qi = (qt * WAVES + wave) * 32 + col;
-  if (qi < a.Sq) {
-    bf16* orow = (bf16*)a.o + b * a.os[0] + head * a.os[2] + (int64_t)qi * a.os[1];
-#pragma unroll
-    for (int db = 0; db < kDB; ++db)
-#pragma unroll
-      for (int pr = 0; pr < 2; ++pr) *(u32x4*)(orow + db * 32 + (2 * pr + hf) * 8) = chunk[db][pr];
-  }
+  store_out_lines<kDB>(O, inv, (bf16*)a.o + b * a.os[0] + head * a.os[2], (qt * WAVES + wave) * 32, a.Sq, a.os[1],
+                       lane);
 }
 
 // ---- persistent kernel for short key sequences (key masks: kv_len only).
@@ -968,23 +975,30 @@ void flash_stream_kernel(const FlashArgs a) {
     const Item it = entry(e);
     const int r0 = it.qt * 256;                   // the item's first query row
     const int rows = uni(min(256, a.Sq - r0));    // its rows below Sq
-    const int qloc = wave * 32 + col;
     // (offsets below 2^31: the plan keeps the output's row stride <= 2^22 elements)
     const uint64_t base =
         o_addr + (uint64_t)((int64_t)it.b * a.os[0] + (int64_t)it.h * a.os[2] + (int64_t)r0 * a.os[1]) * 2u;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(uintptr_t)base, (short)0, (int)(((int64_t)(rows - 1) * a.os[1] + D) * 2), 0x00020000);
-    const uint32_t row_off = qloc < rows ? (uint32_t)(qloc * (int)a.os[1]) * 2u : 0x80000000u;
+    // whole 128-byte lines (line_chunks): lane l stores rows (l & 7) + 8 i of
+    // its wave; one 64-wide d pair at a time (few registers)
+    uint32_t off[4];
 #pragma unroll
-    for (int db = 0; db < kDB; ++db) {
-      u32x4 chunk[1][2];
-      const f32x16 Ob[1] = {O[db]};
-      pack_out_rows<1>(Ob, inv, chunk);
+    for (int i = 0; i < 4; ++i) {
+      const int q = wave * 32 + (lane & 7) + 8 * i;
+      off[i] = q < rows ? (uint32_t)(q * (int)a.os[1]) * 2u : 0x80000000u;
+    }
 #pragma unroll
-      for (int pr = 0; pr < 2; ++pr)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, chunk[0][pr]), rs,
-                                               row_off + (uint32_t)(db * 32 + (2 * pr + hf) * 8) * 2u, 0,
-                                               0);
+    for (int p = 0; p < kDB / 2; ++p) {
+      u32x4 chunk[2][2];
+      const f32x16 Ob[2] = {O[2 * p], O[2 * p + 1]};
+      pack_out_rows<2>(Ob, inv, chunk);
+      u32x4 out[4];
+      line_chunks(chunk, out);
+      const uint32_t cofs = line_chunk_offset(lane, p);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, out[i]), rs, off[i] + cofs, 0, 0);
     }
   };
   auto probs = [&](const f32x16 (&S)[2], float cc_, float m, bf16x8 (&P)[2][2]) __attribute__((always_inline)) -> float {

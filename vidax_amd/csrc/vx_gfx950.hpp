@@ -87,6 +87,43 @@ __device__ __forceinline__ void pack_out_rows(const f32x16 (&O)[kDB], float inv,
     }
 }
 
+// Regroups the packed output chunks of two 32-wide d blocks (c[b][pr] as
+// pack_out_rows leaves them for blocks 2p + b) into whole 128-byte lines:
+// out[i] of lane l holds 8-d chunk ((l >> 4) & 1) * 2 + (l >> 5) of block
+// 2p + ((l >> 3) & 1) of the wave's query row (l & 7) + 8 i, so that a
+// 16-byte store of out[i] per lane writes 8 rows x 128 contiguous bytes
+// (instead of 32 rows x 32 bytes). Per dword one v_permlane16_swap trades
+// chunks between 16-lane rows (pr 0 of rows 1 and 3 with pr 1 of rows 0 and
+// 2: lane l then holds row l & 15, then l & 15 + 16) and two DPP moves
+// rotate the 16-lane rows by 8 under a bank mask (rows 0-7 of both blocks,
+// then rows 8-15). All 64 lanes must be active.
+__device__ __forceinline__ void line_chunks(u32x4 (&c)[2][2], u32x4 (&out)[4]) {
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const auto r = __builtin_amdgcn_permlane16_swap(c[b][0][w], c[b][1][w], false, false);
+      c[b][0][w] = r[0];
+      c[b][1][w] = r[1];
+    }
+  constexpr int kRowRor8 = 0x128;  // DPP row_ror:8
+#pragma unroll
+  for (int xy = 0; xy < 2; ++xy)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      // lanes 8-15 of each row (banks 2, 3) take block 1 of the row 8 lanes down
+      out[2 * xy][w] = __builtin_amdgcn_update_dpp(c[0][xy][w], c[1][xy][w], kRowRor8, 0xf, 0xc, false);
+      // lanes 0-7 (banks 0, 1) take block 0 of the row 8 lanes up
+      out[2 * xy + 1][w] = __builtin_amdgcn_update_dpp(c[1][xy][w], c[0][xy][w], kRowRor8, 0xf, 0x3, false);
+    }
+}
+
+// Byte offset, within its row, of the chunk line_chunks leaves in lane l
+// for the block pair p.
+__device__ __forceinline__ uint32_t line_chunk_offset(int lane, int p) {
+  return (uint32_t)((2 * p + ((lane >> 3) & 1)) * 64 + (((lane >> 4) & 1) * 2 + (lane >> 5)) * 16);
+}
+
 __device__ __forceinline__ bf16x4 lds_read_tr16(const unsigned char* p) {
   s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS s16x4*)(p));
   return __builtin_bit_cast(bf16x4, r);
