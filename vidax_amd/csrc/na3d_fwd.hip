@@ -63,6 +63,32 @@ __device__ __forceinline__ float sum16(const float (&p)[16]) {
 // The per-head sum of squares adds the 8-element chunk sums in the order of
 // that kernel's xor-butterfly over the head's D/8 chunks (chunk c = 2*ds+hf
 // pairs with c^8, c^4, c^2 inside the lane and with c^1 in the other half).
+// Output rows of a wave's 32 queries, query r being the token (t, y0 +
+// r / QX, x0 + r % QX) of the head's output og (tokens tok_stride apart;
+// rows outside the Hs x W grid are dropped): the O^T accumulators
+// normalised by inv, packed and regrouped into whole 128-byte lines
+// (pack_out_rows, line_chunks), one 64-wide d pair at a time.
+template <int kDB, int QX>
+__device__ __forceinline__ void store_na_rows(const f32x16 (&O)[kDB], float inv, bf16* og, int64_t tok_stride,
+                                              int t, int y0, int x0, int Hs, int W, int lane) {
+#pragma unroll
+  for (int p = 0; p < kDB / 2; ++p) {
+    u32x4 c2[2][2];
+    const f32x16 Ob[2] = {O[2 * p], O[2 * p + 1]};
+    pack_out_rows<2>(Ob, inv, c2);  // all lanes: cross-lane exchanges
+    u32x4 out[4];
+    line_chunks(c2, out);
+    const uint32_t cofs = line_chunk_offset(lane, p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = (lane & 7) + 8 * i;
+      const int y = y0 + r / QX, x = x0 + r % QX;
+      if (y < Hs && x < W)
+        *(u32x4*)((unsigned char*)(og + (((int64_t)t * Hs + y) * W + x) * tok_stride) + cofs) = out[i];
+    }
+  }
+}
+
 template <int NDS>
 __device__ __forceinline__ void prep_q(bf16x8 (&qr)[NDS], int hf, int64_t tok, const Na3dArgs& a) {
   constexpr int D = NDS * 16;
@@ -322,6 +348,8 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
 
   const float lt = halves_sum(l_run);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  // (per-lane row stores: the line regrouping's registers would add spills
+  // to this kernel at head dim 128)
   u32x4 chunk[kNDB][2];
   pack_out_rows<kNDB>(O, inv, chunk);  // all lanes: cross-lane exchange
   if (q_in) {
@@ -851,15 +879,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 
   const float lt = halves_sum(l_run);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-  u32x4 chunk[kDB][2];
-  pack_out_rows<kDB>(O, inv, chunk);  // all lanes: cross-lane exchange
-  if (q_in) {
-    bf16* orow = og + token(t, yq, xq) * tok_stride;
-#pragma unroll
-    for (int db = 0; db < kDB; ++db)
-#pragma unroll
-      for (int pr = 0; pr < 2; ++pr) *(u32x4*)(orow + db * 32 + (2 * pr + hf) * 8) = chunk[db][pr];
-  }
+  store_na_rows<kDB, C::kQX>(O, inv, og, tok_stride, t, y0, xq0, Hs, W, lane);
 }
 
 // Three waves per SIMD for the 32-key segments at head dim 64 (146 VGPRs,
