@@ -22,6 +22,8 @@
 #include "vx_kernels.h"
 #include "vx_qk_prep.hpp"
 
+#include <algorithm>
+#include <atomic>
 #include <string>
 
 namespace vx {
@@ -46,107 +48,193 @@ __device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
 
 // NCHUNK: 16-byte chunks per lane (exact); FULL: the row is a whole number of
 // 1 KiB wave accesses, so no lane is ever idle and no chunk needs a bounds test.
-template <int NCHUNK, bool FULL>
+//
+// Wave w of the grid (n_waves in all) takes rows w, w + n_waves, ... (one
+// resident round of waves, consecutive waves on consecutive rows). Across
+// its rows a wave keeps the weights of its chunks in registers, rounded to
+// bf16 (the rounding rms_elem applies to them), and reads each row's
+// rotation table once per lane: a lane's chunks c = lane + 64 i all sit at
+// the same position (8 lane) mod head_dim of their heads, since 64 chunks
+// span a whole number of heads. With kPrefetch the next row's loads are
+// issued before the current row is normalised, rotated and stored, after
+// that row's table loads, so that waiting for the tables leaves the next row
+// in flight.
+// PER_HEAD: the norm is taken per head (a.per_head), whose weight vector of
+// head_dim values then gives every chunk of a lane the same 8 weights.
+template <int NCHUNK, bool FULL, bool PER_HEAD>
 __global__ __launch_bounds__(kWavesPerBlock * 64) void qk_prologue_kernel(const PrologueArgs a) {
+  // The next row's loads are issued early (two row buffers) for whole-row
+  // norms of up to 10 chunks per lane; the per-head norm (more work per row:
+  // one reduction per head) and longer rows keep one buffer and more waves
+  // per SIMD.
+  constexpr bool kPrefetch = !PER_HEAD && NCHUNK <= 10;
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (row >= (int64_t)a.B * a.S) return;  // whole waves only
-  const int b = (int)(row / a.S);
-  const int s = (int)(row - (int64_t)b * a.S);
+  const int64_t rows = (int64_t)a.B * a.S;
+  const int64_t n_waves = (int64_t)gridDim.x * kWavesPerBlock;
+  const int64_t r0 = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (r0 >= rows) return;  // whole waves only
   const int row_len = a.H * a.D;
   const int n_chunks = row_len / 8;
   auto live = [&](int c) { return FULL || c < n_chunks; };
-  const bf16* xr = (const bf16*)a.x + b * a.x_bstride + s * a.x_sstride;
-  bf16* orow = (bf16*)a.out + b * a.o_bstride + s * a.o_sstride;
+  const bool norm = a.weight != nullptr, rope = a.cos != nullptr;
+  const int hpos = (lane * 8) % a.D;  // position of this lane's chunks within their heads
 
-  bf16x8 v[NCHUNK];
-  float ss[NCHUNK];
+  constexpr int kW = PER_HEAD ? 1 : NCHUNK;  // weight chunks held
+  bf16x8 wb[kW];
+  if (norm) {
 #pragma unroll
-  for (int i = 0; i < NCHUNK; ++i) {
-    const int c = lane + 64 * i;
-    ss[i] = 0.f;
-    if (live(c)) {
-      v[i] = __builtin_nontemporal_load((const bf16x8*)(xr + c * 8));  // read once: streaming
-      ss[i] = sum_sq8(v[i]);
+    for (int i = 0; i < kW; ++i) {
+      const int c = lane + 64 * i;
+      if (PER_HEAD || live(c)) {
+        const float* wp = a.weight + (PER_HEAD ? hpos : c * 8);
+        const f32x4 w0 = *(const f32x4*)wp, w1 = *(const f32x4*)(wp + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wb[i][e] = to_bf16(e < 4 ? w0[e] : w1[e - 4]);
+      }
     }
   }
+  const float ps = (float)to_bf16(a.post_scale);
 
-  if (a.weight != nullptr) {
-    float rinv_row = 0.f;
-    if (!a.per_head) {
-      float t = 0.f;
-#pragma unroll
-      for (int i = 0; i < NCHUNK; ++i) t += ss[i];
-      rinv_row = rms_inv(wave_sum(t), row_len, a.eps);
-    }
+  auto row_bs = [&](int64_t r, int& b, int& s) {
+    b = (int)(r / a.S);
+    s = (int)(r - (int64_t)b * a.S);
+  };
+  auto load_row = [&](int64_t r, bf16x8 (&v)[NCHUNK]) __attribute__((always_inline)) {
+    int b, s;
+    row_bs(r, b, s);
+    const bf16* xr = (const bf16*)a.x + b * a.x_bstride + s * a.x_sstride;
 #pragma unroll
     for (int i = 0; i < NCHUNK; ++i) {
       const int c = lane + 64 * i;
-      // per head: the head_dim / 8 lanes of an aligned group share a head
-      float rinv = rinv_row;
-      if (a.per_head) rinv = rms_inv(group_sum(ss[i], a.D / 8), a.D, a.eps);
-      if (live(c)) {
-        const f32x4 w0 = *(const f32x4*)(a.weight + c * 8);
-        const f32x4 w1 = *(const f32x4*)(a.weight + c * 8 + 4);
+      if (live(c)) v[i] = __builtin_nontemporal_load((const bf16x8*)(xr + c * 8));  // read once: streaming
+    }
+  };
+  // row r, whose x is in v: table loads, then the next row's x (into vn),
+  // then the norm, scale and rotation of v and its store
+  auto process = [&](int64_t r, bf16x8 (&v)[NCHUNK], int64_t r_next, bf16x8 (&vn)[NCHUNK]) __attribute__((always_inline)) {
+    int b, s;
+    row_bs(r, b, s);
+    f32x4 cs = {}, sn = {};
+    if (rope) {
+      cs = *(const f32x4*)(a.cos + (int64_t)s * a.tab_stride + hpos / 2);
+      sn = *(const f32x4*)(a.sin + (int64_t)s * a.tab_stride + hpos / 2);
+    }
+    if (r_next < rows) load_row(r_next, vn);
+    float ss[NCHUNK];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[i][e] = rms_elem((float)v[i][e], rinv, e < 4 ? w0[e] : w1[e - 4]);
+    for (int i = 0; i < NCHUNK; ++i) ss[i] = live(lane + 64 * i) ? sum_sq8(v[i]) : 0.f;
+    if (norm) {
+      float rinv_row = 0.f;
+      if (!PER_HEAD) {
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < NCHUNK; ++i) t += ss[i];
+        rinv_row = rms_inv(wave_sum(t), row_len, a.eps);
+      }
+#pragma unroll
+      for (int i = 0; i < NCHUNK; ++i) {
+        // per head: the head_dim / 8 lanes of an aligned group share a head
+        float rinv = rinv_row;
+        if (PER_HEAD) rinv = rms_inv(group_sum(ss[i], a.D / 8), a.D, a.eps);
+        if (live(lane + 64 * i)) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[i][e] = rms_elem((float)v[i][e], rinv, (float)wb[PER_HEAD ? 0 : i][e]);
+        }
       }
     }
-  }
-
-  if (a.post_scale != 1.0f) {
-    const float ps = (float)to_bf16(a.post_scale);
+    if (a.post_scale != 1.0f) {
 #pragma unroll
-    for (int i = 0; i < NCHUNK; ++i) {
-      if (live(lane + 64 * i)) {
+      for (int i = 0; i < NCHUNK; ++i) {
+        if (live(lane + 64 * i)) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[i][e] = scale_elem((float)v[i][e], ps);
+          for (int e = 0; e < 8; ++e) v[i][e] = scale_elem((float)v[i][e], ps);
+        }
       }
     }
-  }
-
-  if (a.cos != nullptr) {
-    const float* cr = a.cos + (int64_t)s * a.tab_stride;
-    const float* sr = a.sin + (int64_t)s * a.tab_stride;
+    if (rope) {
+#pragma unroll
+      for (int i = 0; i < NCHUNK; ++i) {
+        if (live(lane + 64 * i)) {
+#pragma unroll
+          for (int p = 0; p < 4; ++p) rope_pair(v[i], p, cs[p], sn[p]);
+        }
+      }
+    }
+    bf16* orow = (bf16*)a.out + b * a.o_bstride + s * a.o_sstride;
 #pragma unroll
     for (int i = 0; i < NCHUNK; ++i) {
       const int c = lane + 64 * i;
-      if (live(c)) {
-        const int j0 = ((c * 8) % a.D) / 2;  // first pair of the chunk within its head
-        const f32x4 cs = *(const f32x4*)(cr + j0);
-        const f32x4 sn = *(const f32x4*)(sr + j0);
-#pragma unroll
-        for (int p = 0; p < 4; ++p) rope_pair(v[i], p, cs[p], sn[p]);
-      }
+      if (live(c)) __builtin_nontemporal_store(v[i], (bf16x8*)(orow + c * 8));  // written once
     }
-  }
+  };
 
-#pragma unroll
-  for (int i = 0; i < NCHUNK; ++i) {
-    const int c = lane + 64 * i;
-    if (live(c)) __builtin_nontemporal_store(v[i], (bf16x8*)(orow + c * 8));  // written once
+  bf16x8 va[NCHUNK];
+  if constexpr (kPrefetch) {
+    bf16x8 vb[NCHUNK];
+    load_row(r0, va);
+    for (int64_t r = r0; r < rows; r += 2 * n_waves) {
+      process(r, va, r + n_waves, vb);
+      if (r + n_waves < rows) process(r + n_waves, vb, r + 2 * n_waves, va);
+    }
+  } else {
+    for (int64_t r = r0; r < rows; r += n_waves) {
+      load_row(r, va);
+      process(r, va, rows, va);
+    }
   }
 }
 
-template <int NCHUNK, bool FULL>
+template <int NCHUNK, bool FULL, bool PER_HEAD>
 const char* prologue_kernel_name() {
-  static const std::string name =
-      "qk_prologue_kernel<" + std::to_string(NCHUNK) + ", " + (FULL ? "true" : "false") + ">";
+  static const std::string name = "qk_prologue_kernel<" + std::to_string(NCHUNK) + ", " + (FULL ? "true" : "false") +
+                                  ", " + (PER_HEAD ? "true" : "false") + ">";
   return name.c_str();
+}
+
+// Workgroups of the instantiation that are resident on one compute unit
+// (from its register use; cached per device, host threads storing the same
+// value).
+template <int NCHUNK, bool FULL, bool PER_HEAD>
+int resident_groups_per_cu() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, qk_prologue_kernel<NCHUNK, FULL, PER_HEAD>,
+                                                     kWavesPerBlock * 64, 0) !=
+            hipSuccess ||
+        n < 1)
+      n = 1;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// One resident round of waves, at most one wave per row.
+template <int NCHUNK, bool FULL, bool PER_HEAD>
+int launch_rows(const PrologueArgs& a, hipStream_t st, const char** launched) {
+  const int64_t rows = (int64_t)a.B * a.S;
+  const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  const int64_t groups = std::min<int64_t>((rows + kWavesPerBlock - 1) / kWavesPerBlock,
+                                           cus * resident_groups_per_cu<NCHUNK, FULL, PER_HEAD>());
+  hipLaunchKernelGGL((qk_prologue_kernel<NCHUNK, FULL, PER_HEAD>), dim3((unsigned)groups),
+                     dim3(kWavesPerBlock * 64), 0, st, a);
+  *launched = prologue_kernel_name<NCHUNK, FULL, PER_HEAD>();
+  return (int)hipGetLastError();
+}
+
+template <int NCHUNK, bool PER_HEAD>
+int launch_ph(const PrologueArgs& a, hipStream_t st, const char** launched) {
+  return (a.H * a.D) % 512 == 0 ? launch_rows<NCHUNK, true, PER_HEAD>(a, st, launched)
+                                : launch_rows<NCHUNK, false, PER_HEAD>(a, st, launched);
 }
 
 template <int NCHUNK>
 int launch(const PrologueArgs& a, hipStream_t st, const char** launched) {
-  const int64_t rows = (int64_t)a.B * a.S;
-  dim3 grid((unsigned)((rows + kWavesPerBlock - 1) / kWavesPerBlock));
-  if ((a.H * a.D) % 512 == 0) {
-    hipLaunchKernelGGL((qk_prologue_kernel<NCHUNK, true>), grid, dim3(kWavesPerBlock * 64), 0, st, a);
-    *launched = prologue_kernel_name<NCHUNK, true>();
-  } else {
-    hipLaunchKernelGGL((qk_prologue_kernel<NCHUNK, false>), grid, dim3(kWavesPerBlock * 64), 0, st, a);
-    *launched = prologue_kernel_name<NCHUNK, false>();
-  }
-  return (int)hipGetLastError();
+  // (without a weight the norm is skipped and PER_HEAD has no effect)
+  return a.per_head && a.weight != nullptr ? launch_ph<NCHUNK, true>(a, st, launched)
+                                           : launch_ph<NCHUNK, false>(a, st, launched);
 }
 
 }  // namespace
