@@ -255,45 +255,43 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
   auto stage_k = [&](const Lanes& ln, int t, int buf_off) { stage(k_addr, k_tile_bytes, ln.k, a.ks[1], t, buf_off); };
   auto stage_v = [&](const Lanes& ln, int t, int buf_off) { stage(v_addr, v_tile_bytes, ln.v, a.vs[1], t, buf_off); };
 
-  // A per-key bias enters the scores through the QK^T accumulator: it starts
-  // at bias / scale for the lane's keys kb*32 + g*8 + hf*4 + 0..3 of tile j
-  // (the tile's mask slot, in LDS by then), so that scale * log2(e) * S is
-  // the scaled logit plus bias * log2(e) and bias tiles stay on the fast path.
-  // With a per-(query, key) bias every tile takes the masked path anyway, and
-  // the key bias is added there, next to the full bias (fewer registers).
+  // A per-key bias is added to a tile's scores (bias / scale for the lane's
+  // keys kb*32 + g*8 + hf*4 + 0..3, from the tile's mask slot) at the top of
+  // the step that takes the tile's softmax, so that scale * log2(e) * S is
+  // the scaled logit plus bias * log2(e) and bias tiles stay on the fast
+  // path; the QK^T accumulators of every tile start at the MFMA's inline
+  // zero (a bias or zero start in registers cost 32 moves per tile). With a
+  // per-(query, key) bias every tile takes the masked path anyway, and the
+  // key bias is added there, next to the full bias (fewer registers).
   //
   // Key-mask tiles are classified on the device from the words staged in the
   // tile's mask slot, lane l holding word l of the tile and one ballot giving
-  // the class: a tile whose 64 biases are all zero starts its accumulators at
-  // zero (no bias reads or scaling), and a tile whose 64 validity bytes are
-  // all set takes the unmasked softmax. So a key mask costs little on the
-  // tiles it leaves unmasked (a padding run of -inf, or a validity hole,
-  // touches few tiles), without the caller inspecting it on the host.
+  // the class: a tile whose 64 biases are all zero takes no bias reads or
+  // adds, and a tile whose 64 validity bytes are all set takes the unmasked
+  // softmax. So a key mask costs little on the tiles it leaves unmasked (a
+  // padding run of -inf, or a validity hole, touches few tiles), without the
+  // caller inspecting it on the host.
   const float inv_scale = 1.0f / a.scale;
   auto bias_word = [&](int j) -> float {
     return *(const VX_LDS float*)(lds + kMaskBuf + (j & (kMaskRing - 1)) * kMaskSlot + 64 + lane * 4);
   };
   auto valid_byte = [&](int j) -> uint32_t { return lds[kMaskBuf + (j & (kMaskRing - 1)) * kMaskSlot + lane]; };
-  constexpr bool kKeyBiasStart = (MASK & kMaskBias) && !kFull;   // key bias through the accumulator start
-  constexpr bool kValidClass = (MASK & kMaskValid) && !kFull;    // (a full bias masks every tile anyway)
-  auto acc_init = [&](int j, f32x16 (&S)[2], bool nonzero) {
-    if (kKeyBiasStart && nonzero) {
-      const lds_u8* bslot = lds + kMaskBuf + (j & (kMaskRing - 1)) * kMaskSlot + 64;
+  constexpr bool kKeyBias = (MASK & kMaskBias) && !kFull;     // key bias added to the scores of nonzero tiles
+  constexpr bool kValidClass = (MASK & kMaskValid) && !kFull;  // (a full bias masks every tile anyway)
+  auto add_key_bias = [&](int j, f32x16 (&S)[2]) {
+    const lds_u8* bslot = lds + kMaskBuf + (j & (kMaskRing - 1)) * kMaskSlot + 64;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 b = *(const VX_LDS f32x4*)(bslot + (kb * 32 + g * 8 + hf * 4) * 4) * inv_scale;
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 b = *(const VX_LDS f32x4*)(bslot + (kb * 32 + g * 8 + hf * 4) * 4);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) S[kb][g * 4 + e] = b[e];
-        }
-    } else {
-      S[0] = f32x16{};
-      S[1] = f32x16{};
-    }
+        for (int e = 0; e < 4; ++e) S[kb][g * 4 + e] = __builtin_fmaf(b[e], inv_scale, S[kb][g * 4 + e]);
+      }
   };
-  auto qk = [&](int tile, int buf_off, f32x16 (&S)[2]) {
-    acc_init(tile, S, kKeyBiasStart && __builtin_amdgcn_ballot_w64(bias_word(tile) != 0.f) != 0);
+  auto qk = [&](int buf_off, f32x16 (&S)[2]) {
+    S[0] = f32x16{};
+    S[1] = f32x16{};
     const lds_u8* kb0 = lds + buf_off;
 #pragma unroll
     for (int ds = 0; ds < kDS; ++ds) {
@@ -409,7 +407,7 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
     }
     __syncthreads();
     f32x16 S[2];
-    qk(t_begin, kKBuf, S);
+    qk(kKBuf, S);
     bf16x8 Pp[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -420,10 +418,8 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
     int vb_prev = kNB - 1;  // V buffer holding V_{t-1}  (= (t+kNB-1) % kNB)
     // the current tile has an invalid key (each step classifies the next one)
     bool invalid_cur = kValidClass && __builtin_amdgcn_ballot_w64(valid_byte(t_begin) == 0) != 0;
-    // the next tile has a nonzero key bias (each step classifies the tile
-    // after next, whose mask has landed one step before its K)
-    bool bias_nz_next =
-        kKeyBiasStart && __builtin_amdgcn_ballot_w64(bias_word(min(t_begin + 1, n_tiles - 1)) != 0.f) != 0;
+    // the current tile has a nonzero key bias (each step classifies the next one)
+    bool bias_nz_cur = kKeyBias && __builtin_amdgcn_ballot_w64(bias_word(t_begin) != 0.f) != 0;
     // One key tile: consumes S (scores of tile t) and Pp (probabilities of
     // tile t-1), produces Sn (scores of tile t+1) and P (probabilities of
     // tile t). The loop below calls it twice per trip with the two register
@@ -440,22 +436,24 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
       // iteration's copies.
       wait_prev();
       __syncthreads();
-      // the class words of tile t+1's validity and tile t+2's bias (their
-      // mask slots have landed: masks run a tile ahead of K), read first so
-      // that their latency is covered by the work below; both classes are
-      // taken at the end of this step, for the next one
-      float bias_next2 = 0.f;
+      // the class words of tile t+1's validity and bias (its mask slot has
+      // landed: masks run a tile ahead of K), read first so that their
+      // latency is covered by the work below; both classes are taken at the
+      // end of this step, for the next one
+      float bias_next = 0.f;
       uint32_t valid_next = 1;
-      if (kKeyBiasStart) bias_next2 = bias_word(min(t + 2, n_tiles - 1));
+      if (kKeyBias) bias_next = bias_word(min(t + 1, n_tiles - 1));
       if (kValidClass) valid_next = valid_byte(t + 1);
+      // tile t's key bias, into its scores (a tile classified nonzero)
+      if (kKeyBias && bias_nz_cur) add_key_bias(t, S);
       const int kb_next = kb_cur == 0 ? kNB - 1 : kb_cur - 1;     // t % kNB
       const int vb_next = vb_prev == 0 ? kNB - 1 : vb_prev - 1;  // (t+kNB-2) % kNB
 
       // ---- key masks. Tiles that hold a masked key (the tail tile, a
       // key_valid hole) take the scores to log2 units here, masked keys ->
       // -inf, and use cc = 1 below; fully valid tiles (and key bias tiles,
-      // whose bias is in the accumulator start) keep the fused scale in the
-      // exp argument.
+      // whose bias is in the scores already) keep the fused scale in the exp
+      // argument.
       const int key0 = t * kBN;
       const lds_u8* mslot = lds + kMaskBuf + (t & (kMaskRing - 1)) * kMaskSlot;  // tile t's mask
       bool slow = key0 + kBN > kv_end;
@@ -561,7 +559,8 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
         };
         if (WAVES == 4 || COPY) softmax_block();
         // read by the QK^T slots (16 and on)
-        acc_init(t + 1, Sn, bias_nz_next);
+        Sn[0] = f32x16{};
+        Sn[1] = f32x16{};
 #pragma unroll
         for (int s = 0; s < kSlots; ++s) {
           if (s + 3 < kSlots) fr[s + 3] = frag(s + 3);
@@ -608,7 +607,7 @@ __device__ __forceinline__ void flash_tile(const FlashArgs& a, const int qtile, 
       kb_cur = kb_cur == kNB - 1 ? 0 : kb_cur + 1;
       vb_prev = vb_prev == kNB - 1 ? 0 : vb_prev + 1;
       if (kValidClass) invalid_cur = __builtin_amdgcn_ballot_w64(valid_next == 0) != 0;
-      if (kKeyBiasStart) bias_nz_next = __builtin_amdgcn_ballot_w64(bias_next2 != 0.f) != 0;
+      if (kKeyBias) bias_nz_cur = __builtin_amdgcn_ballot_w64(bias_next != 0.f) != 0;
     };
 
     f32x16 S2[2];
