@@ -324,8 +324,15 @@ def _copy_calibration(mib, steps):
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: 20; with the default warm-up, more for short calls: "
+                         "enough for --timed-ms)")
+    ap.add_argument("--timed-ms", type=float, default=100.0)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps before the timed ones (default: at least 3 and at least "
+                         "--warmup-ms of GPU work, so the timed steps run at the clock the chip holds "
+                         "under sustained load)")
+    ap.add_argument("--warmup-ms", type=float, default=250.0)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -423,13 +430,44 @@ def main(argv=None):
         def step():
             na3d_attention(q, k, v, p["kernel"], out=out)
 
-    for _ in range(max(1, args.warmup)):
-        step()
-    torch.cuda.synchronize()
-    kernel_name = _lib.last_launch()  # the kernel the step launched (the last one, for two launches)
+    # Warm-up. Under sustained load the chip holds a power-limited shader
+    # clock, but after any idle period of a few milliseconds it starts a burst
+    # fast, drops below that clock for ~10 ms and recovers over ~20 ms more:
+    # a 0.34 ms call ran 0.34 ms for 5 steps, 0.39-0.45 ms for the next 10
+    # and 0.35 ms only after 40. So the untimed steps run back to back, in
+    # chunks of ~20 ms with one synchronisation each, until --warmup-ms of
+    # wall time has passed (unless --warmup is given), everything the timed
+    # loop needs is made before them, and the timed loop covers at least
+    # --timed-ms (unless --steps is given).
     stream = torch.cuda.current_stream(dev)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     clock = _ClockStamps(dev)
+    if args.warmup is not None:
+        n_warm = max(1, args.warmup)
+        if args.steps is None:
+            args.steps = 20
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+        for _ in range(n_warm):
+            step()
+    else:
+        step()  # (the first call also loads the kernels)
+        torch.cuda.synchronize()
+        t_w = time.perf_counter()
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        n_warm = 3
+        est = max((time.perf_counter() - t_w) / 2, 1e-5)
+        if args.steps is None:
+            args.steps = max(20, int(args.timed_ms * 1e-3 / est) + 1)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+        chunk = max(1, int(0.02 / est))
+        while (time.perf_counter() - t_w) * 1e3 < args.warmup_ms:
+            for _ in range(chunk):
+                step()
+            n_warm += chunk
+            torch.cuda.synchronize()
+    kernel_name = _lib.last_launch()  # the kernel the step launched (the last one, for two launches)
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     clock.stamp(0, stream)
     ev[0].record(stream)
@@ -485,7 +523,7 @@ def main(argv=None):
         "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": n_warm,
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
