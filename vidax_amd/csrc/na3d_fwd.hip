@@ -700,8 +700,21 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     }
     const StepRows cur = rr;
     rr = next_rows(kcur);
-    issue(kg, C::kK + (s & 1) * C::kSlot, rr);   // K of step s + 2
-    issue(vg, C::kV + (s & 1) * C::kSlot, cur);  // V of step s
+    // This wave's copies of the step, V of step s (copies 0 .. kCopiesPerWave-1)
+    // then K of step s + 2: copy j is issued in MFMA slot j, so that a wave's
+    // matrix and softmax work does not queue behind its copies (a wave issues
+    // in order, and the CU's load path takes each 1 KiB copy in ~16 cycles).
+    auto copy = [&](int j) __attribute__((always_inline)) {
+      const bool isv = j < C::kCopiesPerWave;
+      const int p = isv ? j : j - C::kCopiesPerWave;
+      if (kExtraWaves == 0 || p + 1 < C::kCopiesPerWave || extra) {
+        const StepRows& r = isv ? cur : rr;
+        lds_dma16_buf(raw_rsrc((isv ? vg : kg) + (dma_row[p] ? r.tok1 : r.tok0)), dma_voff[p],
+                      lds_base + (isv ? C::kV : C::kK) + (s & 1) * C::kSlot + dma_dst[p]);
+      }
+    };
+    constexpr int kStepCopies = 2 * C::kCopiesPerWave;
+    static_assert(kStepCopies <= C::kSlots, "one copy per MFMA slot at most");
 
     const VX_LDS unsigned char* kb = lds + C::kK + ((s + 1) & 1) * C::kSlot;  // K of chunk s+1
     const VX_LDS unsigned char* vb = lds + C::kV + ((s + 1) & 1) * C::kSlot;  // V of chunk s-1
@@ -711,6 +724,8 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     if (!(IN && (TALL || wave_in))) {
       // no query of this wave is inside the grid (the ragged x or y edge):
       // it only copies its share of the rows
+#pragma unroll
+      for (int j = 0; j < kStepCopies; ++j) copy(j);
       P[0] = bf16x8{};
       P[1] = bf16x8{};
       return;
@@ -749,6 +764,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
           O[i % kDB] = mfma32x32x16(fr[i], Pp[i / kDB], O[i % kDB]);
         else
           Sn = mfma32x32x16(fr[i], qr[i - C::kPV], Sn);
+        if (i < kStepCopies) copy(i);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
@@ -781,6 +797,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
           O[i % kDB] = mfma32x32x16(fr[i], Pp[i / kDB], O[i % kDB]);
         else
           Sn = mfma32x32x16(fr[i], qr[i - C::kPV], Sn);
+        if (i < kStepCopies) copy(i);
 #pragma unroll
         for (int u = 0; u < C::kScoresPerSlot; ++u) {
           const int e = i * C::kScoresPerSlot + u;
