@@ -309,6 +309,12 @@ def test_na3d_kernel_name_follows_the_launch_rule():
     assert na3d_kernel_name(160, 11, 64) == "na3d_tall_wide_kernel<64>"  # 160 = 5 x 32
     assert na3d_kernel_name(104, 11, 64) == "na3d_tall_kernel<64>"       # 112 vs 128 columns
     assert na3d_kernel_name(24, 13, 64) == "na3d_tall_wide_kernel<64>"   # 32 columns either way
+    # deep t windows (kt' >= 5) take the 32-wide bricks two t planes deep
+    assert na3d_kernel_name(160, 11, 64, depth=33, kernel_t=11) == "na3d_deep_kernel<64>"
+    assert na3d_kernel_name(160, 11, 64, depth=33, kernel_t=3) == "na3d_tall_wide_kernel<64>"
+    assert na3d_kernel_name(160, 11, 64, depth=4, kernel_t=11) == "na3d_tall_wide_kernel<64>"  # kt' = 4
+    assert na3d_kernel_name(80, 11, 64, depth=33, kernel_t=11) == "na3d_tall_kernel<64>"      # not 32-wide
+    assert na3d_kernel_name(160, 11, 128, depth=33, kernel_t=11) == "na3d_tall_kernel<128>"
     assert na3d_kernel_name(160, 11) == "na3d_tall_kernel<128>"          # head dim 128: narrow bricks
     assert na3d_kernel_name(80, 13) == "na3d_tall_kernel<128>"
     assert na3d_kernel_name(12, 40) == "na3d_tall_kernel<128>"        # clamped to the grid width

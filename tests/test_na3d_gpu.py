@@ -55,9 +55,9 @@ NA_CASES = [
 ]
 
 
-def _expected_kernel(H, W, kw, D):
-    """The NA kernel for a clamped x window kw' = min(kw, W), written out
-    here independently of the library's plan."""
+def _expected_kernel(H, W, kw, D, T=1, kt=1):
+    """The NA kernel for a clamped x window kw' = min(kw, W) (and t window
+    kt' = min(kt, T)), written out here independently of the library's plan."""
     k = min(kw, W)
     if k <= 9:
         # head dim 64: 1 x 8 x 16 bricks unless they cover more of the y-x
@@ -68,7 +68,8 @@ def _expected_kernel(H, W, kw, D):
     if k <= 13:
         # head dim 64: 32-wide bricks unless they leave more ragged columns
         if D == 64 and -(-W // 32) * 32 == -(-W // 16) * 16:
-            return "na3d_tall_wide_kernel<64>"
+            # deep t windows: the 32-wide bricks two t planes deep
+            return "na3d_deep_kernel<64>" if min(kt, T) >= 5 else "na3d_tall_wide_kernel<64>"
         return f"na3d_tall_kernel<{D}>"
     if k <= 25:
         return f"na3d_pipe_kernel<32, {D}>"
@@ -81,7 +82,7 @@ def _run(gpu, shape, ks, seed, D):
     q, k, v = O.make_na3d_inputs(B, T, H, W, NH, D, seed)
     out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), ks)
     launched = _lib.last_launch()
-    assert launched == _expected_kernel(H, W, ks[2], D), launched
+    assert launched == _expected_kernel(H, W, ks[2], D, T, ks[0]), launched
     torch.cuda.synchronize()
     _check(out.float().cpu().numpy(), O.na3d(q, k, v, ks), f"oracle ({launched})")
 
@@ -107,6 +108,8 @@ NA_D64_CASES = [
     ((1, 3, 4, 64, 1), (3, 3, 5), 65),        # 16-key segments, one y brick
     ((1, 4, 22, 40, 2), (3, 7, 7), 66),       # tall bricks at kw' = 7, ragged x (40 % 16)
     ((2, 3, 13, 21, 1), (3, 5, 9), 67),       # tall bricks at kw' = 9, ragged y and x, even area
+    ((1, 7, 10, 32, 2), (7, 9, 11), 68),      # deep bricks: odd T (a last brick one plane deep), ragged y
+    ((2, 6, 9, 30, 1), (5, 5, 13), 69),       # deep bricks at kt' = 5, ragged y and x, two batch items
 ]
 
 
@@ -237,16 +240,17 @@ def test_na3d_config4_whole_grid(gpu):
 @pytest.mark.slow
 def test_na3d_stage5_sampled_rows(gpu):
     """LTX-2.5 VAE stage-5 shape at full size: grid 33x88x160, window
-    (11,11,11), B=1 NH=4 D=64 (the 1 x 8 x 32 tall bricks); every query of
+    (11,11,11), B=1 NH=4 D=64 (the 2 x 4 x 32 deep bricks); every query of
     64 sampled (t, y) rows against the oracle: 8 rows for each y mod 8 (each
-    wave's position in its 8-row brick), the t and y borders included; a row
-    holds every x brick of the grid."""
+    row's position in a brick of 4 y rows, twice), both t parities (the two
+    planes of a brick), the t and y borders included; a row holds every x
+    brick of the grid."""
     from vidax_amd import _lib, neighborhood_attention_3d
     _say("na3d stage 5 33x88x160 NH=4 D=64 (11,11,11) sampled rows")
     B, T, H, W, NH = 1, 33, 88, 160, 4
     q, k, v = O.make_na3d_inputs(B, T, H, W, NH, 64, 5)
     out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), (11, 11, 11))
-    assert _lib.last_launch() == _expected_kernel(H, W, 11, 64), _lib.last_launch()
+    assert _lib.last_launch() == _expected_kernel(H, W, 11, 64, T, 11), _lib.last_launch()
     o = out.float().cpu().numpy()
     rng = np.random.default_rng(55)
     rows = {(0, 0), (32, 87), (16, 7), (16, 8), (5, 44), (27, 80), (1, 86), (31, 3)}
@@ -256,7 +260,7 @@ def test_na3d_stage5_sampled_rows(gpu):
         yy = [ys[0], ys[-1]] + [int(x) for x in rng.choice(ys[1:-1], size=6, replace=False)]
         rows.update(zip(ts, yy))
     rows = sorted(rows)
-    assert len(rows) >= 64 and len({y % 8 for _, y in rows}) == 8
+    assert len(rows) >= 64 and len({y % 8 for _, y in rows}) == 8 and len({t % 2 for t, _ in rows}) == 2
     ref = O.na3d_dense(q, k, v, (11, 11, 11), acc=np.float32, ty_rows=rows)
     sel = tuple(np.array(rows).T)
     _check(o[0][sel], ref[0][sel], f"stage-5 {len(rows)} rows")

@@ -63,14 +63,14 @@ __device__ __forceinline__ float sum16(const float (&p)[16]) {
 // The per-head sum of squares adds the 8-element chunk sums in the order of
 // that kernel's xor-butterfly over the head's D/8 chunks (chunk c = 2*ds+hf
 // pairs with c^8, c^4, c^2 inside the lane and with c^1 in the other half).
-// Output rows of a wave's 32 queries, query r being the token (t, y0 +
-// r / QX, x0 + r % QX) of the head's output og (tokens tok_stride apart;
-// rows outside the Hs x W grid are dropped): the O^T accumulators
-// normalised by inv, packed and regrouped into whole 128-byte lines
-// (pack_out_rows, line_chunks), one 64-wide d pair at a time.
-template <int kDB, int QX>
+// Output rows of a wave's 32 queries, query r being the token (t + r /
+// (QX QY), y0 + r / QX % QY, x0 + r % QX) of the head's output og (tokens
+// tok_stride apart; rows outside the T x Hs x W grid are dropped): the O^T
+// accumulators normalised by inv, packed and regrouped into whole 128-byte
+// lines (pack_out_rows, line_chunks), one 64-wide d pair at a time.
+template <int kDB, int QX, int QY = 32 / QX>
 __device__ __forceinline__ void store_na_rows(const f32x16 (&O)[kDB], float inv, bf16* og, int64_t tok_stride,
-                                              int t, int y0, int x0, int Hs, int W, int lane) {
+                                              int t, int y0, int x0, int T, int Hs, int W, int lane) {
 #pragma unroll
   for (int p = 0; p < kDB / 2; ++p) {
     u32x4 c2[2][2];
@@ -82,9 +82,9 @@ __device__ __forceinline__ void store_na_rows(const f32x16 (&O)[kDB], float inv,
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = (lane & 7) + 8 * i;
-      const int y = y0 + r / QX, x = x0 + r % QX;
-      if (y < Hs && x < W)
-        *(u32x4*)((unsigned char*)(og + (((int64_t)t * Hs + y) * W + x) * tok_stride) + cofs) = out[i];
+      const int tt = t + r / (QX * QY), y = y0 + r / QX % QY, x = x0 + r % QX;
+      if (tt < T && y < Hs && x < W)
+        *(u32x4*)((unsigned char*)(og + (((int64_t)tt * Hs + y) * W + x) * tok_stride) + cofs) = out[i];
     }
   }
 }
@@ -387,14 +387,21 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
 // the 42-key x union of a row is staged in 48 slots for 32 queries (26 in
 // 32 for 16 with the narrow brick), one workgroup barrier per step for
 // twice the queries.
-template <int SEG, int D, bool TALL = false, bool WIDE = false>
+// DEEP: wide bricks two t planes deep, 2 (t) x 4 (y) x 32 (x), waves of 2 t x
+// 4 y x 4 x queries: for a t window of kt' planes the union of a wave's
+// windows is (kt' + 1) x (kh' + 3) rows instead of kt' x (kh' + 7), e.g. 12 x
+// 14 against 11 x 18 rows at (11, 11, 11).
+template <int SEG, int D, bool TALL = false, bool WIDE = false, bool DEEP = false>
 struct PipeCfg {
   static_assert(!TALL || SEG == 16, "the tall geometry reads 16-key segments");
   static_assert(!WIDE || TALL, "wide bricks are tall bricks");
+  static_assert(!DEEP || WIDE, "deep bricks are wide bricks");
   static constexpr int kWaves = WIDE ? 8 : 4;
   static constexpr int kThreads = kWaves * 64;
-  static constexpr int kBrickY = TALL ? 8 : 4, kBrickX = TALL ? (WIDE ? 32 : 16) : 32;
-  static constexpr int kQX = kBrickX / kWaves;           // x columns per wave (32 / kQX y rows)
+  static constexpr int kQT = DEEP ? 2 : 1;               // t planes per brick (and per wave)
+  static constexpr int kBrickY = TALL ? (DEEP ? 4 : 8) : 4, kBrickX = TALL ? (WIDE ? 32 : 16) : 32;
+  static constexpr int kQX = kBrickX / kWaves;           // x columns per wave
+  static constexpr int kQY = 32 / (kQX * kQT);           // y rows per wave (and per brick)
   static constexpr int kRB = D * 2;                      // bytes of one key
   static constexpr int kRows = SEG == 16 ? 2 : 1;        // key rows per step
   // key slots per LDS row (>= kBrickX - kQX + SEG, a multiple of 8)
@@ -418,9 +425,10 @@ struct PipeCfg {
   static_assert(kNS % kKeysPerCopy == 0 && kHalfL % 256 == 0, "whole copies per row, bank-aligned planes");
 };
 
-template <int SEG, int D, bool TALL, bool WIDE = false>
+template <int SEG, int D, bool TALL, bool WIDE = false, bool DEEP = false>
 __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int n_xb) {
-  using C = PipeCfg<SEG, D, TALL, WIDE>;
+  using C = PipeCfg<SEG, D, TALL, WIDE, DEEP>;
+  static_assert(C::kQY == C::kBrickY, "the waves of a brick sit side by side in x");
   static_assert(C::kBrickX - C::kQX + SEG <= C::kNS, "a wave's segment stays inside the LDS row");
   __shared__ __attribute__((aligned(16))) unsigned char smem[C::kSmem];
   VX_LDS unsigned char* const lds = (VX_LDS unsigned char*)smem;
@@ -436,7 +444,8 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   // x walks the bricks of heads x, x+8, ... in order: the workgroups resident
   // on one XCD then cover neighbouring bricks of one head and share their
   // key rows in that XCD's L2.
-  const int n_bricks = a.T * n_yb * n_xb;
+  const int n_tb = (a.T + C::kQT - 1) / C::kQT;  // t bricks
+  const int n_bricks = n_tb * n_yb * n_xb;
   int brick, head;
   if (a.order == kNaOrderTColumns) {
     // Deep t windows: XCD x takes the x-th eighth of the (head, brick
@@ -448,9 +457,9 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     const int xcd = lin & 7, j = lin >> 3;
     const int g = xcd * (total >> 3) + min(xcd, total & 7) + j;  // the eighths are contiguous ranges of g
     const int ncol = n_yb * n_xb;
-    const int rest = g / a.T;
+    const int rest = g / n_tb;
     head = rest / ncol;
-    brick = (g - rest * a.T) * ncol + (rest - head * ncol);     // (t * n_yb + yb) * n_xb + xb
+    brick = (g - rest * n_tb) * ncol + (rest - head * ncol);    // (tb * n_yb + yb) * n_xb + xb
   } else if ((a.NH & 7) == 0) {
     const int lin = blockIdx.y * n_bricks + blockIdx.x;  // launch order within a batch item
     const int xcd = lin & 7, j = lin >> 3;
@@ -466,17 +475,18 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   head = uni(head);
   const int xb = uni(brick % n_xb);
   const int yb = uni((brick / n_xb) % n_yb);
-  const int t = uni(brick / (n_xb * n_yb));
+  const int t = uni(brick / (n_xb * n_yb)) * C::kQT;  // the brick's first t plane
   const int b = blockIdx.z;
   const int T = a.T, Hs = a.Hs, W = a.W, kt = a.kt, kh = a.kh, kw = a.kw;
   const int y0 = yb * C::kBrickY, x0 = xb * C::kBrickX;
 
-  // ---- the workgroup's key rows (box rows r = tr * NY + yr).
+  // ---- the workgroup's key rows (box rows r = tr * NY + yr over NT planes).
   const int t_lo = uni(window_start(t, T, kt));
+  const int NT = C::kQT == 1 ? kt : uni(window_start(min(t + C::kQT - 1, T - 1), T, kt) + kt - t_lo);
   const int Y_lo = uni(window_start(y0, Hs, kh));
   const int NY = uni(window_start(min(y0 + C::kBrickY - 1, Hs - 1), Hs, kh) + kh - Y_lo);
   const int X_lo = uni(window_start(x0, W, kw));
-  const int nrows = kt * NY;
+  const int nrows = NT * NY;
   const int n_steps = (nrows + C::kRows - 1) / C::kRows;
 
   // ---- this wave's queries: y rows y0..y0+kBrickY-1, x columns xq0..xq0+kQX-1.
@@ -484,11 +494,12 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   const int ox = uni(window_start(min(xq0, W - 1), W, kw) - X_lo);  // wave's first x slot, <= kBrickX - kQX
 
   // ---- this lane's query and its window.
-  const int yq = y0 + col / C::kQX, xq = xq0 + col % C::kQX;
-  const bool q_in = yq < Hs && xq < W;
+  const int tq = t + col / (C::kQX * C::kQY), yq = y0 + col / C::kQX % C::kQY, xq = xq0 + col % C::kQX;
+  const bool q_in = tq < T && yq < Hs && xq < W;
   const bool wave_in = y0 < Hs && xq0 < W;  // wave-uniform: some query of the wave is in the grid
-  const int yqc = min(yq, Hs - 1), xqc = min(xq, W - 1);
+  const int tqc = min(tq, T - 1), yqc = min(yq, Hs - 1), xqc = min(xq, W - 1);
   const int sy = window_start(yqc, Hs, kh) - Y_lo;
+  const int st = window_start(tqc, T, kt) - t_lo;  // (deep bricks: the lane's first plane in the box)
   const int sx = window_start(xqc, W, kw) - X_lo - ox;  // in [0, SEG - kw]
   // The x window of score register i (key (i/4)*8 + hf*4 + i%4 of the
   // chunk). kAccMask: a 0 / -inf vector that every chunk's QK^T MFMAs start
@@ -524,7 +535,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 
   bf16x8 qr[C::kQK];
   {
-    const bf16* p = qg + token(t, yqc, xqc) * tok_stride + hf * 8;
+    const bf16* p = qg + token(tqc, yqc, xqc) * tok_stride + hf * 8;
 #pragma unroll
     for (int ds = 0; ds < C::kQK; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
   }
@@ -558,7 +569,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   // offset) that advance one row at a time and stop at the last row, so no
   // step divides by NY.
   struct Cursor {
-    int r, yr;
+    int r, yr, tr;
     int64_t tok;
   };
   const int64_t row_step = (int64_t)W * tok_stride;             // next y
@@ -572,14 +583,16 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
       c.tok += row_step;
       if (++c.yr == NY) {
         c.yr = 0;
+        ++c.tr;
         c.tok += plane_jump;
       }
     }
     c.r = __builtin_amdgcn_readfirstlane(c.r);
     c.yr = __builtin_amdgcn_readfirstlane(c.yr);
+    c.tr = __builtin_amdgcn_readfirstlane(c.tr);
     c.tok = (int64_t)uniform_u64((uint64_t)c.tok);
   };
-  const Cursor first = {0, 0, ((int64_t)t_lo * Hs + Y_lo) * W * tok_stride};
+  const Cursor first = {0, 0, 0, ((int64_t)t_lo * Hs + Y_lo) * W * tok_stride};
   // The key rows of one step (their token offsets and y in the box), taken
   // from the cursor, which moves on by kRows rows. K walks the rows; V and
   // the window mask use each step's record two steps later, so only one
@@ -587,14 +600,17 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   struct StepRows {
     int64_t tok0, tok1;
     int yr0, yr1;
+    int tr0, tr1;  // (deep bricks: the rows' planes in the box)
   };
   auto next_rows = [&](Cursor& c) -> StepRows {
     StepRows rr;
     rr.tok0 = c.tok;
     rr.yr0 = c.yr;
+    rr.tr0 = c.tr;
     advance(c);
     rr.tok1 = C::kRows == 2 ? c.tok : rr.tok0;
     rr.yr1 = C::kRows == 2 ? c.yr : rr.yr0;
+    rr.tr1 = C::kRows == 2 ? c.tr : rr.tr0;
     if (C::kRows == 2) advance(c);
     return rr;
   };
@@ -669,7 +685,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   for (int off = threadIdx.x * 16; off < C::kSlot; off += C::kThreads * 16)
     *(VX_LDS u32x4*)(lds + C::kV + C::kSlot + off) = u32x4{0, 0, 0, 0};
   // q preparation while the first key rows land (its loads overlap theirs)
-  if (a.q_prep != 0) prep_q(qr, hf, token(t, yqc, xqc), a);
+  if (a.q_prep != 0) prep_q(qr, hf, token(tqc, yqc, xqc), a);
   wait_vmem<0>();
   __syncthreads();
   f32x16 S = s_init;
@@ -696,7 +712,8 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
       const int r = s * C::kRows + (SEG == 16 ? h2 : 0);
-      row_ok[h2] = r < nrows && (unsigned)((h2 == 0 ? rr.yr0 : rr.yr1) - sy) < (unsigned)kh;
+      row_ok[h2] = r < nrows && (unsigned)((h2 == 0 ? rr.yr0 : rr.yr1) - sy) < (unsigned)kh &&
+                   (C::kQT == 1 || (unsigned)((h2 == 0 ? rr.tr0 : rr.tr1) - st) < (unsigned)kt);
     }
     const StepRows cur = rr;
     rr = next_rows(kcur);
@@ -896,7 +913,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 
   const float lt = halves_sum(l_run);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-  store_na_rows<kDB, C::kQX>(O, inv, og, tok_stride, t, y0, xq0, Hs, W, lane);
+  store_na_rows<kDB, C::kQX, C::kQY>(O, inv, og, tok_stride, t, y0, xq0, T, Hs, W, lane);
 }
 
 // Three waves per SIMD for the 32-key segments at head dim 64 (146 VGPRs,
@@ -928,6 +945,14 @@ void na3d_tall_wide_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   na3d_pipe_body<16, D, true, true>(a, n_yb, n_xb);
 }
 
+// Head dim 64, deep t windows: the wide bricks two t planes deep (2 x 4 x 32,
+// waves of 2 t x 4 y x 4 x), two workgroups of 48 KiB per CU.
+template <int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void na3d_deep_kernel(const Na3dArgs a, int n_yb, int n_xb) {
+  na3d_pipe_body<16, D, true, true, true>(a, n_yb, n_xb);
+}
+
 }  // namespace
 
 int launch_na3d_fwd(const Na3dArgs& a, void* stream, const char** launched) {
@@ -954,6 +979,15 @@ int launch_na3d_fwd(const Na3dArgs& a, void* stream, const char** launched) {
       dim3 grid((unsigned)a.T * n_yb * n_xb, a.NH, a.B);
       hipLaunchKernelGGL((na3d_tall_wide_kernel<64>), grid, dim3(512), 0, st, a, n_yb, n_xb);
       *launched = "na3d_tall_wide_kernel<64>";
+      return (int)hipGetLastError();
+    }
+    case kNaDeep: {
+      if (a.D != 64) return (int)hipErrorNotSupported;
+      const int n_yb = (a.Hs + 3) / 4;
+      const int n_xb = (a.W + 31) / 32;
+      dim3 grid((unsigned)((a.T + 1) / 2) * n_yb * n_xb, a.NH, a.B);
+      hipLaunchKernelGGL((na3d_deep_kernel<64>), grid, dim3(512), 0, st, a, n_yb, n_xb);
+      *launched = "na3d_deep_kernel<64>";
       return (int)hipGetLastError();
     }
     case kNaPipe16:

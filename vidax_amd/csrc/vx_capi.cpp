@@ -225,13 +225,19 @@ SplitPlan flash_split_plan(int32_t B, int32_t Sq, int32_t Sk, int32_t H, int32_t
 // (same box, (3,7,7) and (3,5,5) windows: 5x22x40 NH=16 -10 %, 9x22x40 NH=8
 // -6 %, 21x45x80 NH=24 -5 %, 17x44x80 NH=8 even; 5x11x20 NH=32, where the
 // tall bricks cover 16 rows for 11, +37 %).
-int32_t na3d_variant(int32_t kw_clamped, int32_t D, int32_t Hs, int32_t W) {
+// Deep t windows (kt' >= kNaDeepMinKt) at head dim 64 with the 32-wide bricks
+// take them two t planes deep: a wave's 2 x 4 x 4 queries need (kt' + 1) x
+// (kh' + 3) key rows instead of the kt' x (kh' + 7) of 1 x 8 x 4.
+int32_t na3d_variant(int32_t kt_clamped, int32_t kw_clamped, int32_t D, int32_t Hs, int32_t W) {
   if (kw_clamped <= 9) {
     const int64_t tall_area = (int64_t)((Hs + 7) / 8 * 8) * ((W + 15) / 16 * 16);
     const int64_t pipe_area = (int64_t)((Hs + 3) / 4 * 4) * ((W + 31) / 32 * 32);
     return D == 64 && tall_area <= pipe_area ? vx::kNaTall : vx::kNaPipe16;
   }
-  if (kw_clamped <= 13) return D == 64 && (W + 31) / 32 * 32 == (W + 15) / 16 * 16 ? vx::kNaTallWide : vx::kNaTall;
+  if (kw_clamped <= 13) {
+    if (D != 64 || (W + 31) / 32 * 32 != (W + 15) / 16 * 16) return vx::kNaTall;
+    return kt_clamped >= vx::kNaDeepMinKt ? vx::kNaDeep : vx::kNaTallWide;
+  }
   if (kw_clamped <= 25) return vx::kNaPipe32;
   return vx::kNaWave;
 }
@@ -241,6 +247,7 @@ const char* na3d_kernel_label(int32_t variant, int32_t D) {
     case vx::kNaPipe16: return D == 64 ? "na3d_pipe_kernel<16, 64>" : "na3d_pipe_kernel<16, 128>";
     case vx::kNaTall: return D == 64 ? "na3d_tall_kernel<64>" : "na3d_tall_kernel<128>";
     case vx::kNaTallWide: return "na3d_tall_wide_kernel<64>";
+    case vx::kNaDeep: return "na3d_deep_kernel<64>";
     case vx::kNaPipe32: return D == 64 ? "na3d_pipe_kernel<32, 64>" : "na3d_pipe_kernel<32, 128>";
     default: return D == 64 ? "na3d_wave_kernel<64>" : "na3d_wave_kernel<128>";
   }
@@ -383,7 +390,7 @@ int32_t na3d_check(const void* q, const void* k, const void* v, const void* out,
     args->kh = kh < Hs ? kh : Hs;
     args->kw = kw < W ? kw : W;
     args->scale = scale;
-    args->variant = na3d_variant(args->kw, D, Hs, W);
+    args->variant = na3d_variant(args->kt, args->kw, D, Hs, W);
     args->order = args->kt >= vx::kNaTColumnsMinKt ? vx::kNaOrderTColumns : vx::kNaOrderLaunch;
     args->q_prep = 0;
     args->q_weight = nullptr;
@@ -596,15 +603,16 @@ int32_t vx_flash_attn_plan(int32_t batch, int32_t seq_q, int32_t seq_k, int32_t 
 
 int32_t vx_na3d_plan(int32_t t, int32_t h, int32_t w, int32_t head_dim, int32_t kernel_t, int32_t kernel_h,
                      int32_t kernel_w, char* kernel_name, int32_t name_len) {
-  (void)kernel_t;
   (void)kernel_h;
   const int32_t rc = na3d_check(reinterpret_cast<const void*>(16), reinterpret_cast<const void*>(16),
                                 reinterpret_cast<const void*>(16), reinterpret_cast<const void*>(16), 1, t, h, w,
                                 1, head_dim, kernel_t, kernel_h, kernel_w, 1.0f, nullptr);
   if (rc != VX_OK) return rc;
   const int32_t kw = kernel_w < w ? kernel_w : w;
+  const int32_t kt = kernel_t < t ? kernel_t : t;
   if (kernel_name != nullptr && name_len > 0)
-    snprintf(kernel_name, (size_t)name_len, "%s", na3d_kernel_label(na3d_variant(kw, head_dim, h, w), head_dim));
+    snprintf(kernel_name, (size_t)name_len, "%s",
+             na3d_kernel_label(na3d_variant(kt, kw, head_dim, h, w), head_dim));
   return ok();
 }
 

@@ -85,7 +85,10 @@ enum Na3dVariant : int32_t {
   kNaPipe32 = 2,  // 13 < kw' <= 25: 32-key x segments
   kNaWave = 3,    // 25 < kw' <= 57, head dim 128: per-wave bricks
   kNaTallWide = 4,  // head dim 64, 9 < kw' <= 13, round_up(W, 32) == round_up(W, 16): 1 x 8 x 32 bricks
+  kNaDeep = 5,      // as kNaTallWide with kt' >= kNaDeepMinKt: 2 x 4 x 32 bricks
 };
+// t windows (clamped) from which the plan takes the deep bricks
+constexpr int32_t kNaDeepMinKt = 5;
 
 // Order in which the pipelined NA kernels' workgroups take their bricks.
 enum Na3dOrder : int32_t {

@@ -17,22 +17,25 @@ from . import _lib
 __all__ = ["neighborhood_attention_3d", "na3d_attention", "na3d_kernel_name", "na3d_block_attention"]
 
 
-def na3d_kernel_name(width: int, kernel_w: int, head_dim: int = 128, height: Optional[int] = None) -> str:
+def na3d_kernel_name(width: int, kernel_w: int, head_dim: int = 128, height: Optional[int] = None,
+                     depth: int = 1, kernel_t: int = 1) -> str:
     """Name of the kernel the library launches for this x window (the C ABI's
     launch plan): row streaming with 16-key x segments up to kw' = 9 (at head
     dim 64 the tall bricks instead when they pad the height x width plane no
     more), its tall-brick form up to kw' = 13 (at head dim 64 in 32-wide
-    bricks when the width rounds up to the same multiple of 16 and 32),
+    bricks when the width rounds up to the same multiple of 16 and 32, two t
+    planes deep for t windows kt' = min(kernel_t, depth) of 5 and more),
     32-key segments up to kw' = 25, the per-wave kernel above that
     (kw' = min(kw, W)). The grid height decides the choice at head dim 64
-    with kw' <= 9 and must be given there."""
+    with kw' <= 9 and must be given there; depth (the grid's t extent) and
+    kernel_t matter at head dim 64 with 9 < kw' <= 13."""
     kw_c = min(int(kernel_w), int(width))
     if height is None:
         if int(head_dim) == 64 and kw_c <= 9:
             raise ValueError("na3d_kernel_name: at head_dim 64 with an x window of at most 9 the kernel "
                              "depends on the grid height; pass height=")
         height = 1
-    return _lib.na3d_plan(1, int(height), int(width), int(head_dim), 1, 1, int(kernel_w))
+    return _lib.na3d_plan(int(depth), int(height), int(width), int(head_dim), int(kernel_t), 1, int(kernel_w))
 
 
 def _aligned16(t: torch.Tensor) -> torch.Tensor:
