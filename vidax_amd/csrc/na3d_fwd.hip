@@ -15,7 +15,8 @@
 //   its bricks pad the grid no more): the same body on 1 x 8 x 16 bricks
 //   with waves of 8 y x 4 x queries, so that a wave's x window still fits a
 //   16-key segment; na3d_tall_wide_kernel<64> runs 1 x 8 x 32 bricks of 8
-//   such waves at head dim 64.
+//   such waves at head dim 64, and na3d_deep_kernel<64> (t windows of 5
+//   and more) 2 x 4 x 32 bricks of waves of 2 t x 4 y x 4 x queries.
 // - na3d_wave_kernel<D> (kw' > 25, any size, D 128 or 64): each wave owns a
 //   1 x 4 x 8 brick on its own and walks its (kt', ny, nx) key box in chunks
 //   of 32 keys, laid out as (t', y') rows of SEG = round_up(nx, 16)
