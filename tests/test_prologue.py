@@ -378,7 +378,8 @@ NA_BLOCK_CASES = [
     # (B, (T, H, W), NH, HD, kernel, norm, rope)  -> launched kernel family
     (1, (3, 8, 20), 4, 64, (3, 7, 7), True, True),        # pipe, 16-key segments, D=64
     (1, (3, 9, 37), 2, 128, (3, 7, 7), True, True),       # pipe, D=128, ragged x
-    (1, (5, 13, 21), 2, 64, (5, 11, 11), True, True),     # tall bricks (stage-5 family), D=64
+    (1, (5, 13, 21), 2, 64, (5, 11, 11), True, True),     # deep bricks (stage-5 family), D=64, odd T
+    (1, (4, 9, 24), 2, 64, (3, 11, 11), True, True),      # 32-wide tall bricks (t window 3), D=64
     (1, (2, 7, 30), 8, 128, (1, 3, 17), True, True),      # 32-key segments, head remap (NH % 8 == 0)
     (1, (2, 4, 40), 1, 128, (1, 3, 31), True, True),      # per-wave kernel (kw' > 25)
     (2, (2, 5, 9), 3, 64, (3, 3, 5), False, True),        # rope only
