@@ -144,10 +144,10 @@ __device__ __forceinline__ void prep_q(bf16x8 (&qr)[NDS], int hf, int64_t tok, c
   }
 }
 
-// Two waves per SIMD (256 registers a wave): its waves stream K from global
-// memory, so the second wave covers those loads' latency (at D = 128 the
-// kernel had 346 registers and one wave per SIMD: 1.9x slower at a (3,7,31)
-// window); the allocator spills one 8-byte value outside the key loop.
+// Two waves per SIMD (at most 256 registers a wave; 230 at D = 128, no
+// spills): its waves stream K from global memory, so the second wave covers
+// those loads' latency (at D = 128 the kernel had 346 registers and one wave
+// per SIMD: 1.9x slower at a (3,7,31) window).
 template <int D>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
@@ -223,8 +223,10 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
     return token(t_lo + tr, y_lo + yr, min(x_lo + j, W - 1));
   };
 
-  // K fragment of chunk c for this lane: key row col of the chunk.
-  bf16x8 kf[kNDS], kfn[kNDS];
+  // K fragment of chunk c for this lane: key row col of the chunk (one
+  // register set: the next chunk's loads are issued once this chunk's QK^T
+  // has read it).
+  bf16x8 kf[kNDS];
   auto load_k = [&](int c, bf16x8* dst) {
     int row, j0;
     half_row(c * kChunk + (col & 16), row, j0);
@@ -278,13 +280,11 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
   store_v(vbuf0);
   for (int c = 0; c < n_chunks; ++c) {
     const bool has_next = c + 1 < n_chunks;
-    if (has_next) {
-      load_k(c + 1, kfn);
-      load_v(c + 1);
-    }
+    if (has_next) load_v(c + 1);
     f32x16 S = f32x16{};
 #pragma unroll
     for (int ds = 0; ds < kNDS; ++ds) S = mfma32x32x16(kf[ds], qr[ds], S);
+    if (has_next) load_k(c + 1, kf);
 
     // ---- window mask, scores to log2 units. Score register i of half h2
     // holds x slot j0 + hf*4 + (i/4)*8 + i%4 of its box row.
@@ -340,11 +340,7 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
         O[db] = mfma32x32x16(vf, P[j], O[db]);
       }
 
-    if (has_next) {
-      store_v((c & 1) ? vbuf0 : vbuf1);
-#pragma unroll
-      for (int ds = 0; ds < kNDS; ++ds) kf[ds] = kfn[ds];
-    }
+    if (has_next) store_v((c & 1) ? vbuf0 : vbuf1);
   }
 
   const float lt = halves_sum(l_run);
