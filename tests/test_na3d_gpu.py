@@ -110,6 +110,8 @@ NA_D64_CASES = [
     ((2, 3, 13, 21, 1), (3, 5, 9), 67),       # tall bricks at kw' = 9, ragged y and x, even area
     ((1, 7, 10, 32, 2), (7, 9, 11), 68),      # deep bricks: odd T (a last brick one plane deep), ragged y
     ((2, 6, 9, 30, 1), (5, 5, 13), 69),       # deep bricks at kt' = 5, ragged y and x, two batch items
+    ((1, 5, 8, 32, 8), (5, 11, 11), 70),      # deep bricks, t window = T, y window clamped, eight heads
+    ((2, 9, 6, 64, 1), (7, 13, 13), 71),      # deep bricks, widest tall x window, y window clamped to 6
 ]
 
 
