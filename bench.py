@@ -341,9 +341,9 @@ def main(argv=None):
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build runs the attention kernels on a single GPU; "
-              "--gpus N with N > 1 is not supported (how the path would shard is "
-              "described in DESIGN.md)", file=sys.stderr)
+        print("bench.py: the attention kernels run on a single GPU here; "
+              "--gpus N with N > 1 is not supported (a sharded run would split "
+              "heads or query tiles over the GPUs, one process each)", file=sys.stderr)
         return 2
 
     if args.copy_calibration_mib:

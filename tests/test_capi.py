@@ -473,9 +473,9 @@ def test_flash_split_plan():
     holds two fp32 partials (O, reference point, row sum per lane) per item."""
     # c1: 61 x 12 = 732 items of 128 queries over 2 x 256 slots: 220 split at tile 61
     assert _split((1, 7800, 7800, 12, 128)) == (220, 61 * 64, 2 * 220 * 4 * 64 * (4 * 16 + 2) * 4)
-    assert _split((1, 32760, 32760, 40, 128)) == (0, 0, 0)     # 5120 items: whole rounds
+    assert _split((1, 32760, 32760, 40, 128)) == (0, 0, 0)     # 5120 items: whole waves of workgroups
     assert _split((2, 32760, 512, 40, 128)) == (0, 0, 0)       # short keys
-    assert _split((1, 119056, 119056, 24, 128)) == (0, 0, 0)   # last round 176 > 128 of 256
+    assert _split((1, 119056, 119056, 24, 128)) == (0, 0, 0)   # last wave of workgroups: 176 > 128 of 256
     assert _split((1, 2048, 1500, 3, 128)) == (48, 768, 2 * 48 * 4 * 64 * 66 * 4)
     assert _split((1, 8192, 2048, 25, 128))[0] == 32            # 8-wave: 800 items, 256 slots
     assert _split((1, 8192, 2048, 25, 64))[2] == 2 * 32 * 8 * 64 * (2 * 16 + 2) * 4

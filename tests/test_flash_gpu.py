@@ -537,7 +537,8 @@ def test_flash_bias_and_mask_broadcast_along_keys(gpu):
     torch.cuda.synchronize()
     o = out.float().cpu().numpy()
     keep = np.broadcast_to(mask[:, 0, :, 0][:, :, None, None], o.shape)
-    # rows with every key masked are written as zeros
+    # rows with every key masked are written as zeros (the library's documented
+    # choice where the reference's softmax would give 0/0)
     assert (o[~keep] == 0).all()
     ref = O.attention(q, k, v)
     err = np.abs(o - ref)[keep]
