@@ -486,13 +486,13 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   const int nrows = NT * NY;
   const int n_steps = (nrows + C::kRows - 1) / C::kRows;
 
-  // ---- this wave's queries: y rows y0..y0+kBrickY-1, x columns xq0..xq0+kQX-1.
+  // ---- this wave's queries: t planes t..t+kQT-1, y rows y0..y0+kBrickY-1,
+  // x columns xq0..xq0+kQX-1.
   const int xq0 = x0 + C::kQX * wave;
   const int ox = uni(window_start(min(xq0, W - 1), W, kw) - X_lo);  // wave's first x slot, <= kBrickX - kQX
 
   // ---- this lane's query and its window.
   const int tq = t + col / (C::kQX * C::kQY), yq = y0 + col / C::kQX % C::kQY, xq = xq0 + col % C::kQX;
-  const bool q_in = tq < T && yq < Hs && xq < W;
   const bool wave_in = y0 < Hs && xq0 < W;  // wave-uniform: some query of the wave is in the grid
   const int tqc = min(tq, T - 1), yqc = min(yq, Hs - 1), xqc = min(xq, W - 1);
   const int sy = window_start(yqc, Hs, kh) - Y_lo;
