@@ -396,7 +396,8 @@ def main(argv=None):
             qk_norm_rope(qx, wq, freqs, p["H"])
             qk_norm_rope(kx, wk, freqs, p["H"])
     elif kind == "na3d_block":
-        from vidax_amd import create_abs_rope3d_freqs, na3d_block_attention, na3d_qk_norm_rope
+        from vidax_amd import create_abs_rope3d_axis_freqs, create_abs_rope3d_freqs, na3d_block_attention
+        from vidax_amd import na3d_qk_norm_rope
         from vidax_amd import neighborhood_attention_3d
         g = torch.Generator(device=dev)
         g.manual_seed(p["seed"])
@@ -406,13 +407,17 @@ def main(argv=None):
         k = torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)  # k as the block prepares it
         v = torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)
         wq = 1.0 + 0.1 * torch.randn(D, generator=g, device=dev)
-        freqs = create_abs_rope3d_freqs(p["T"], p["Hs"], p["W"], D, device=dev)
         out = torch.empty_like(q)
         flops, bytes_ = _na3d_work(p)
         if p["fused"]:
+            # the fused kernel reads the per-axis rows (t, h and w tables)
+            freqs = create_abs_rope3d_axis_freqs(p["T"], p["Hs"], p["W"], D, device=dev)
+
             def step():
                 na3d_block_attention(q, k, v, p["kernel"], wq, freqs, out=out)
         else:
+            freqs = create_abs_rope3d_freqs(p["T"], p["Hs"], p["W"], D, device=dev)
+
             def step():
                 neighborhood_attention_3d(na3d_qk_norm_rope(q, wq, freqs, post_scale=D ** -0.5), k, v, p["kernel"])
     else:

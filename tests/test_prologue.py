@@ -192,6 +192,25 @@ def test_abs_rope_tables_equal_axis_form():
     assert moved.tolist() == [False] * 20 + [True] * 12
 
 
+def test_abs_rope_axis_tables_equal_token_tables():
+    """The per-axis rows the fused NA kernel reads, gathered per token, are
+    bit for bit the per-token tables (both come from one per-axis routine)."""
+    from vidax_amd import create_abs_rope3d_axis_freqs, create_abs_rope3d_freqs
+    for T, H, W, HD, split in [(3, 5, 7, 64, None), (2, 4, 6, 128, None), (4, 3, 5, 64, (16, 24, 24)),
+                               (2, 3, 4, 128, (0, 64, 64))]:
+        cos, sin = create_abs_rope3d_freqs(T, H, W, HD, rope_split=split)
+        ax = create_abs_rope3d_axis_freqs(T, H, W, HD, rope_split=split)
+        d_t, d_h, d_w = ax.split
+        assert d_t + d_h + d_w == HD
+        for tok, tabs in ((cos, ax.cos), (sin, ax.sin)):
+            for n, tab in zip((T, H, W), tabs):
+                assert tab.shape[0] == n and tab.shape[1] % 4 == 0 and tab.dtype == torch.float32
+            gathered = torch.cat([tabs[0][:, None, None, :d_t // 2].expand(T, H, W, d_t // 2),
+                                  tabs[1][None, :, None, :d_h // 2].expand(T, H, W, d_h // 2),
+                                  tabs[2][None, None, :, :d_w // 2].expand(T, H, W, d_w // 2)], dim=-1)
+            assert torch.equal(gathered.reshape(tok.shape), tok)
+
+
 def test_abs_rope_relative_positions():
     """q.k after rotation depends only on the offset along each axis."""
     rng = np.random.default_rng(6)
@@ -396,8 +415,8 @@ def test_na3d_block_attention_fused_q(gpu, B, grid, NH, HD, ks, norm, rope):
     attention bar, and bit for bit against the separate path (the one-pass
     prologue kernel, then the NA kernel), whose rounding points and
     per-head summation order the fused kernel reproduces."""
-    from vidax_amd import (create_abs_rope3d_freqs, na3d_block_attention, na3d_qk_norm_rope,
-                           neighborhood_attention_3d)
+    from vidax_amd import (create_abs_rope3d_axis_freqs, create_abs_rope3d_freqs, na3d_block_attention,
+                           na3d_qk_norm_rope, neighborhood_attention_3d)
     from vidax_amd import _lib
     print(f"[case] na3d fused q B={B} grid={grid} NH={NH} HD={HD} kernel={ks} norm={norm} rope={rope}", flush=True)
     rng = np.random.default_rng(sum(grid) * NH + HD + ks[2])
@@ -419,6 +438,13 @@ def test_na3d_block_attention_fused_q(gpu, B, grid, NH, HD, ks, norm, rope):
     print(f"  launched {launched}", flush=True)
     assert launched == _lib.last_launch()
     assert torch.equal(fused, separate), "fused q preparation differs from the two-pass path"
+    if rope:
+        # the per-axis tables (t, h and w rows) give the same bits
+        axes = create_abs_rope3d_axis_freqs(*grid, HD, device=gpu)
+        fused_ax = na3d_block_attention(tq, tk, tv, ks, tw, axes)
+        torch.cuda.synchronize()
+        assert _lib.last_launch() == launched
+        assert torch.equal(fused_ax, fused), "per-axis rope tables differ from the per-token tables"
     q_ref = P.na3d_qk_norm_rope(q, wq, post_scale=post, rope=rope)
     k_ref = tk.float().cpu().numpy()
     ref = A.na3d(q_ref, k_ref, v, ks)

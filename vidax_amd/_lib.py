@@ -38,6 +38,8 @@ EXPORTED_SYMBOLS = (
     "vx_last_launch",
     "vx_na3d_qprep_fwd",
     "vx_na3d_qprep_check",
+    "vx_na3d_qprep_axes_fwd",
+    "vx_na3d_qprep_axes_check",
     "vx_flash_attn_ws_fwd",
     "vx_flash_attn_workspace_size",
     "vx_flash_attn_split_plan",
@@ -53,6 +55,7 @@ _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
 _i64p = ctypes.POINTER(ctypes.c_int64)
+_i32p = ctypes.POINTER(ctypes.c_int32)
 
 _FLASH_ARGS = [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32,
                _i64p, _i64p, _i64p, _i64p, _f32]
@@ -60,6 +63,7 @@ _NA3D_ARGS = [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i
 _FLASH_BIAS_ARGS = [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64p, _i32, _i32, _i32, _i32, _i32,
                     _i64p, _i64p, _i64p, _i64p, _f32]
 _NA3D_QPREP_ARGS = [_p, _p, _p, _p] + [_i32] * 9 + [_p, _f32, _f32, _p, _p, _i64]
+_NA3D_QPREP_AXES_ARGS = [_p, _p, _p, _p] + [_i32] * 9 + [_p, _f32, _f32] + [_p] * 6 + [_i64p, _i32p]
 _PROLOGUE_ARGS = [_p, _p, _p, _f32, _i32, _p, _p, _i64, _i32, _i32, _i32, _i32, _i64p, _i64p]
 _SCALED_PROLOGUE_ARGS = _PROLOGUE_ARGS[:5] + [_f32] + _PROLOGUE_ARGS[5:]
 
@@ -120,6 +124,10 @@ def lib() -> ctypes.CDLL:
             h.vx_na3d_qprep_fwd.argtypes = _NA3D_QPREP_ARGS + [_p]
             h.vx_na3d_qprep_check.restype = _i32
             h.vx_na3d_qprep_check.argtypes = _NA3D_QPREP_ARGS
+            h.vx_na3d_qprep_axes_fwd.restype = _i32
+            h.vx_na3d_qprep_axes_fwd.argtypes = _NA3D_QPREP_AXES_ARGS + [_p]
+            h.vx_na3d_qprep_axes_check.restype = _i32
+            h.vx_na3d_qprep_axes_check.argtypes = _NA3D_QPREP_AXES_ARGS
             h.vx_flash_attn_ws_fwd.restype = _i32
             h.vx_flash_attn_ws_fwd.argtypes = _FLASH_ARGS + [_p, _i64, _p]
             h.vx_flash_attn_noalloc_fwd.restype = _i32

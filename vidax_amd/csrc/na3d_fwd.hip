@@ -91,7 +91,8 @@ __device__ __forceinline__ void store_na_rows(const f32x16 (&O)[kDB], float inv,
 }
 
 template <int NDS>
-__device__ __forceinline__ void prep_q(bf16x8 (&qr)[NDS], int hf, int64_t tok, const Na3dArgs& a) {
+__device__ __forceinline__ void prep_q(bf16x8 (&qr)[NDS], int hf, int64_t tok, int tq, int yq, int xq,
+                                       const Na3dArgs& a) {
   constexpr int D = NDS * 16;
   // all loads first (weights, then the token's rotation tables), so their
   // latencies overlap
@@ -105,7 +106,23 @@ __device__ __forceinline__ void prep_q(bf16x8 (&qr)[NDS], int hf, int64_t tok, c
       w[ds][1] = *(const f32x4*)(wp + 4);
     }
   }
-  if (rope) {
+  if (rope && (a.q_prep & kQPrepRopeAxes)) {
+    // per-axis tables: the lane's 4 pairs 8 ds + 4 hf + 0..3 lie in one
+    // axis's part (its boundaries are multiples of 4); a few rows per axis,
+    // shared by every token and head, instead of one table row per token
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
+      const int j = ds * 8 + hf * 4;
+      const bool in_t = j < a.q_ax_pairs[0], in_h = !in_t && j < a.q_ax_pairs[1];
+      const int64_t off = in_t ? tq * a.q_ax_stride[0] + j
+                               : (in_h ? yq * a.q_ax_stride[1] + (j - a.q_ax_pairs[0])
+                                       : xq * a.q_ax_stride[2] + (j - a.q_ax_pairs[1]));
+      const float* cb = in_t ? a.q_cos_ax[0] : (in_h ? a.q_cos_ax[1] : a.q_cos_ax[2]);
+      const float* sb = in_t ? a.q_sin_ax[0] : (in_h ? a.q_sin_ax[1] : a.q_sin_ax[2]);
+      cs[ds] = *(const f32x4*)(cb + off);
+      sn[ds] = *(const f32x4*)(sb + off);
+    }
+  } else if (rope) {
     const float* cr = a.q_cos + tok * a.q_tab_stride + hf * 4;
     const float* sr = a.q_sin + tok * a.q_tab_stride + hf * 4;
 #pragma unroll
@@ -209,7 +226,7 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
 #pragma unroll
     for (int ds = 0; ds < kNDS; ++ds) qr[ds] = *(const bf16x8*)(p + ds * 16);
   }
-  if (a.q_prep != 0) prep_q(qr, hf, token(t, yqc, xqc), a);
+  if (a.q_prep != 0) prep_q(qr, hf, token(t, yqc, xqc), t, yqc, xqc, a);
 
   // Box row and first x slot of the 16-key half chunk starting at box key kb2.
   auto half_row = [&](int kb2, int& trow, int& j0) {
@@ -696,7 +713,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   for (int off = threadIdx.x * 16; off < C::kSlot; off += C::kThreads * 16)
     *(VX_LDS u32x4*)(lds + C::kV + C::kSlot + off) = u32x4{0, 0, 0, 0};
   // q preparation while the first key rows land (its loads overlap theirs)
-  if (a.q_prep != 0) prep_q(qr, hf, token(tqc, yqc, xqc), a);
+  if (a.q_prep != 0) prep_q(qr, hf, token(tqc, yqc, xqc), tqc, yqc, xqc, a);
   wait_vmem<0>();
   __syncthreads();
   f32x16 S = s_init;

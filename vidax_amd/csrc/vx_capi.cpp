@@ -398,6 +398,11 @@ int32_t na3d_check(const void* q, const void* k, const void* v, const void* out,
     args->q_eps = 0.f;
     args->q_post_scale = 1.f;
     args->q_tab_stride = 0;
+    for (int i = 0; i < 3; ++i) {
+      args->q_cos_ax[i] = args->q_sin_ax[i] = nullptr;
+      args->q_ax_stride[i] = 0;
+    }
+    args->q_ax_pairs[0] = args->q_ax_pairs[1] = 0;
   }
   return ok();
 }
@@ -433,6 +438,55 @@ int32_t na3d_qprep_check(const float* weight, float eps, float post_scale, const
     args->q_cos = rope_cos;
     args->q_sin = rope_sin;
     args->q_tab_stride = rope_stride;
+    for (int i = 0; i < 3; ++i) {
+      args->q_cos_ax[i] = args->q_sin_ax[i] = nullptr;
+      args->q_ax_stride[i] = 0;
+    }
+    args->q_ax_pairs[0] = args->q_ax_pairs[1] = 0;
+  }
+  return VX_OK;
+}
+
+// The per-axis rotation tables of vx_na3d_qprep_axes_fwd, checked into a:
+// split (d_t, d_h, d_w) even, summing to head_dim, with d_t and d_h multiples
+// of 8 (the kernel takes a lane's 4 pairs from one axis); per axis with
+// d > 0, 16-byte aligned cos/sin rows of d/2 pairs, stride a multiple of 4.
+int32_t na3d_rope_axes_check(const float* const (&cos_ax)[3], const float* const (&sin_ax)[3],
+                             const int64_t* strides, const int32_t* split, int32_t D, vx::Na3dArgs* args) {
+  const bool any = cos_ax[0] || cos_ax[1] || cos_ax[2] || sin_ax[0] || sin_ax[1] || sin_ax[2];
+  if (split == nullptr) {
+    if (any) return fail(VX_ERR_INVALID_ARGUMENT, "rope tables need rope_split");
+    return VX_OK;
+  }
+  if (strides == nullptr) return fail(VX_ERR_INVALID_ARGUMENT, "rope_strides must be given with rope_split");
+  for (int i = 0; i < 3; ++i)
+    if (split[i] < 0 || split[i] % 2 != 0)
+      return fail(VX_ERR_INVALID_ARGUMENT, "rope_split[%d] = %d must be even and >= 0", i, split[i]);
+  if ((int64_t)split[0] + split[1] + split[2] != D)
+    return fail(VX_ERR_INVALID_ARGUMENT, "rope_split (%d, %d, %d) must sum to head_dim %d", split[0], split[1],
+                split[2], D);
+  if (split[0] % 8 != 0 || split[1] % 8 != 0)
+    return fail(VX_ERR_UNSUPPORTED, "rope_split (%d, %d, %d): the t and h parts must be multiples of 8", split[0],
+                split[1], split[2]);
+  for (int i = 0; i < 3; ++i) {
+    if (split[i] == 0) continue;
+    if (cos_ax[i] == nullptr || sin_ax[i] == nullptr)
+      return fail(VX_ERR_INVALID_ARGUMENT, "axis %d has %d rotated channels but no cos/sin table", i, split[i]);
+    if (!aligned16(cos_ax[i]) || !aligned16(sin_ax[i]))
+      return fail(VX_ERR_INVALID_ARGUMENT, "the axis %d cos/sin tables must be 16-byte aligned", i);
+    if (strides[i] < split[i] / 2 || strides[i] % 4 != 0)
+      return fail(VX_ERR_INVALID_ARGUMENT, "rope_strides[%d] (%lld) must be a multiple of 4 and >= %d", i,
+                  (long long)strides[i], split[i] / 2);
+  }
+  if (args != nullptr) {
+    args->q_prep |= vx::kQPrepRope | vx::kQPrepRopeAxes;
+    for (int i = 0; i < 3; ++i) {
+      args->q_cos_ax[i] = cos_ax[i];
+      args->q_sin_ax[i] = sin_ax[i];
+      args->q_ax_stride[i] = strides[i];
+    }
+    args->q_ax_pairs[0] = split[0] / 2;
+    args->q_ax_pairs[1] = (split[0] + split[1]) / 2;
   }
   return VX_OK;
 }
@@ -509,7 +563,7 @@ int32_t injected() {
 
 extern "C" {
 
-int32_t vx_abi_version(void) { return 10700; }
+int32_t vx_abi_version(void) { return 10800; }
 
 const char* vx_last_error(void) { return g_error; }
 
@@ -757,6 +811,47 @@ int32_t vx_na3d_qprep_fwd(const void* q, const void* k, const void* v, void* out
   if ((rc = na3d_qprep_check(q_norm_weight, eps, q_post_scale, rope_cos, rope_sin, rope_stride, head_dim,
                              &args)) != VX_OK)
     return rc;
+  if ((rc = injected()) != VX_OK) return rc;
+  const char* launched = "";
+  const int err = vx::launch_na3d_fwd(args, stream, &launched);
+  if (err != 0) return fail(VX_ERR_LAUNCH, "neighbourhood attention launch failed (hipError_t %d)", err);
+  g_last_launch = launched;
+  return ok();
+}
+
+int32_t vx_na3d_qprep_axes_check(const void* q, const void* k, const void* v, const void* out, int32_t batch,
+                                 int32_t t, int32_t h, int32_t w, int32_t num_heads, int32_t head_dim,
+                                 int32_t kernel_t, int32_t kernel_h, int32_t kernel_w, const float* q_norm_weight,
+                                 float eps, float q_post_scale, const float* rope_cos_t, const float* rope_sin_t,
+                                 const float* rope_cos_h, const float* rope_sin_h, const float* rope_cos_w,
+                                 const float* rope_sin_w, const int64_t* rope_strides, const int32_t* rope_split) {
+  int32_t rc = na3d_check(q, k, v, out, batch, t, h, w, num_heads, head_dim, kernel_t, kernel_h, kernel_w, 1.0f,
+                          nullptr);
+  if (rc != VX_OK) return rc;
+  if ((rc = na3d_qprep_check(q_norm_weight, eps, q_post_scale, nullptr, nullptr, 0, head_dim, nullptr)) != VX_OK)
+    return rc;
+  const float* const cs[3] = {rope_cos_t, rope_cos_h, rope_cos_w};
+  const float* const sn[3] = {rope_sin_t, rope_sin_h, rope_sin_w};
+  if ((rc = na3d_rope_axes_check(cs, sn, rope_strides, rope_split, head_dim, nullptr)) != VX_OK) return rc;
+  return ok();
+}
+
+int32_t vx_na3d_qprep_axes_fwd(const void* q, const void* k, const void* v, void* out, int32_t batch, int32_t t,
+                               int32_t h, int32_t w, int32_t num_heads, int32_t head_dim, int32_t kernel_t,
+                               int32_t kernel_h, int32_t kernel_w, const float* q_norm_weight, float eps,
+                               float q_post_scale, const float* rope_cos_t, const float* rope_sin_t,
+                               const float* rope_cos_h, const float* rope_sin_h, const float* rope_cos_w,
+                               const float* rope_sin_w, const int64_t* rope_strides, const int32_t* rope_split,
+                               void* stream) {
+  vx::Na3dArgs args;
+  int32_t rc = na3d_check(q, k, v, out, batch, t, h, w, num_heads, head_dim, kernel_t, kernel_h, kernel_w, 1.0f,
+                          &args);
+  if (rc != VX_OK) return rc;
+  if ((rc = na3d_qprep_check(q_norm_weight, eps, q_post_scale, nullptr, nullptr, 0, head_dim, &args)) != VX_OK)
+    return rc;
+  const float* const cs[3] = {rope_cos_t, rope_cos_h, rope_cos_w};
+  const float* const sn[3] = {rope_sin_t, rope_sin_h, rope_sin_w};
+  if ((rc = na3d_rope_axes_check(cs, sn, rope_strides, rope_split, head_dim, &args)) != VX_OK) return rc;
   if ((rc = injected()) != VX_OK) return rc;
   const char* launched = "";
   const int err = vx::launch_na3d_fwd(args, stream, &launched);

@@ -38,6 +38,15 @@ def na3d_kernel_name(width: int, kernel_w: int, head_dim: int = 128, height: Opt
     return _lib.na3d_plan(int(depth), int(height), int(width), int(head_dim), int(kernel_t), 1, int(kernel_w))
 
 
+def _pad_rows(t: torch.Tensor) -> torch.Tensor:
+    """A copy of a 2-D fp32 table whose rows are padded to a multiple of 4
+    floats (16-byte aligned rows)."""
+    width = -(-t.shape[1] // 4) * 4
+    out = torch.zeros((t.shape[0], width), dtype=torch.float32, device=t.device)
+    out[:, :t.shape[1]] = t
+    return out
+
+
 def _aligned16(t: torch.Tensor) -> torch.Tensor:
     t = t.contiguous()
     return t if t.data_ptr() % 16 == 0 else t.clone()
@@ -96,8 +105,9 @@ def na3d_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     q as projected (B, T, H, W, NH, HD) goes through per-head RMSNorm with
     `q_norm_weight` (HD,) (skipped when None), times bf16(q_post_scale)
     (default HD ** -0.5, the block's `q * head_dim ** -0.5`), and the absolute
-    RoPE with `freqs` from `create_abs_rope3d_freqs` (skipped when None), as
-    the kernel loads each query row; k (normed and rotated, e.g. by
+    RoPE with `freqs` from `create_abs_rope3d_freqs` or, read per axis and
+    with the same result, `create_abs_rope3d_axis_freqs` (skipped when None),
+    as the kernel loads each query row; k (normed and rotated, e.g. by
     `na3d_qk_norm_rope`) and v are used as given. Equals
     `neighborhood_attention_3d(na3d_qk_norm_rope(q, ...), k, v, kernel_size)`
     without the separate pass over q."""
@@ -117,11 +127,32 @@ def na3d_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         weight = torch.as_tensor(q_norm_weight, device=q.device).to(torch.float32).reshape(-1).contiguous()
         if weight.numel() != HD:
             raise ValueError(f"q_norm_weight has {weight.numel()} entries, head_dim is {HD}")
+    from .prologue import AbsRope3dAxes
+    axes = isinstance(freqs, AbsRope3dAxes)
     cos_t = sin_t = None
     stride = 0
-    if freqs is not None:
+    if freqs is not None and not axes:
         from .prologue import _tables
         cos_t, sin_t, stride = _tables(freqs, T * H * W, HD // 2, q.device)
+    if axes:
+        # per-axis tables: (n_axis, >= d/2) fp32 rows of at least T, H and W
+        # positions, 16-byte aligned, row strides a multiple of 4 floats
+        ax_c, ax_s = [], []
+        for c, s_, n, d in zip(freqs.cos, freqs.sin, (T, H, W), freqs.split):
+            for tab in (c, s_):
+                if (tab.dim() != 2 or tab.shape[0] < n or tab.shape[1] < d // 2 or tab.dtype != torch.float32
+                        or tab.device != q.device):
+                    raise ValueError(f"per-axis rope table {tuple(tab.shape)} does not cover {n} positions "
+                                     f"x {d // 2} pairs (fp32, on q's device)")
+            ax_c.append(c if (c.stride(1) == 1 and c.stride(0) % 4 == 0 and c.data_ptr() % 16 == 0)
+                        else _pad_rows(c))
+            ax_s.append(s_ if (s_.stride(1) == 1 and s_.stride(0) % 4 == 0 and s_.data_ptr() % 16 == 0)
+                        else _pad_rows(s_))
+        ax_strides = (ctypes.c_int64 * 3)(*[int(c.stride(0)) for c in ax_c])
+        for c, s_ in zip(ax_c, ax_s):
+            if s_.stride(0) != c.stride(0):
+                raise ValueError("the cos and sin tables of an axis must have the same row stride")
+        ax_split = (ctypes.c_int32 * 3)(*[int(d) for d in freqs.split])
     if out is None:
         out = torch.empty_like(q)
     elif (out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous() or
@@ -129,12 +160,21 @@ def na3d_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         raise ValueError("out must be a contiguous, 16-byte aligned bf16 tensor shaped like q, on q's device")
     stream = torch.cuda.current_stream(q.device).cuda_stream
     with torch.cuda.device(q.device):
-        rc = _lib.lib().vx_na3d_qprep_fwd(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-            B, T, H, W, NH, HD, int(kernel_size[0]), int(kernel_size[1]), int(kernel_size[2]),
-            weight.data_ptr() if weight is not None else None, ctypes.c_float(eps),
-            ctypes.c_float(q_post_scale),
-            cos_t.data_ptr() if cos_t is not None else None,
-            sin_t.data_ptr() if sin_t is not None else None, stride, ctypes.c_void_p(stream))
+        if axes:
+            rc = _lib.lib().vx_na3d_qprep_axes_fwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                B, T, H, W, NH, HD, int(kernel_size[0]), int(kernel_size[1]), int(kernel_size[2]),
+                weight.data_ptr() if weight is not None else None, ctypes.c_float(eps),
+                ctypes.c_float(q_post_scale),
+                ax_c[0].data_ptr(), ax_s[0].data_ptr(), ax_c[1].data_ptr(), ax_s[1].data_ptr(),
+                ax_c[2].data_ptr(), ax_s[2].data_ptr(), ax_strides, ax_split, ctypes.c_void_p(stream))
+        else:
+            rc = _lib.lib().vx_na3d_qprep_fwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                B, T, H, W, NH, HD, int(kernel_size[0]), int(kernel_size[1]), int(kernel_size[2]),
+                weight.data_ptr() if weight is not None else None, ctypes.c_float(eps),
+                ctypes.c_float(q_post_scale),
+                cos_t.data_ptr() if cos_t is not None else None,
+                sin_t.data_ptr() if sin_t is not None else None, stride, ctypes.c_void_p(stream))
     _lib.raise_for(rc)
     return out

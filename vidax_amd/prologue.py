@@ -14,14 +14,15 @@ reference's norm -> (scale) -> rope sequences.
 from __future__ import annotations
 
 import ctypes
-from typing import Optional, Tuple
+from typing import NamedTuple, Optional, Tuple
 
 import torch
 
 from . import _lib
 
 __all__ = ["create_rope3d_freqs", "apply_rope3d", "rms_norm", "qk_norm_rope",
-           "default_rope_dim_split", "create_abs_rope3d_freqs", "apply_abs_rope3d", "na3d_qk_norm_rope"]
+           "default_rope_dim_split", "create_abs_rope3d_freqs", "create_abs_rope3d_axis_freqs", "AbsRope3dAxes",
+           "apply_abs_rope3d", "na3d_qk_norm_rope"]
 
 
 def _axis_freqs(seq_len: int, dim: int, theta: float, device) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -182,6 +183,56 @@ def default_rope_dim_split(head_dim: int) -> Tuple[int, int, int]:
     return d_t, d_hw, d_hw
 
 
+def _abs_rope_split(head_dim: int, rope_split) -> Tuple[int, int, int]:
+    d_t, d_h, d_w = rope_split or default_rope_dim_split(head_dim)
+    if d_t + d_h + d_w != head_dim or d_t % 2 or d_h % 2 or d_w % 2:
+        raise ValueError(f"rope split {(d_t, d_h, d_w)} must be even and sum to head_dim {head_dim}")
+    return d_t, d_h, d_w
+
+
+def _abs_rope_axis(n: int, d: int, base: float, device) -> Tuple[torch.Tensor, torch.Tensor]:
+    """cos and sin (n, d/2) of positions 0..n-1 times one axis's inverse
+    frequencies 1 / base^(arange(0, d, 2) / d), the frequencies computed in
+    float64 and stored as fp32, the angles formed in fp32
+    (`diffusion_vae.py:106-128`)."""
+    inv = 1.0 / torch.pow(torch.tensor(float(base), dtype=torch.float64),
+                          torch.arange(0, d, 2, dtype=torch.float64) / d)
+    ang = torch.arange(n, dtype=torch.float32, device=device)[:, None] * inv.to(torch.float32).to(device)[None, :]
+    return torch.cos(ang), torch.sin(ang)
+
+
+class AbsRope3dAxes(NamedTuple):
+    """Per-axis tables of the absolute interleaved-pair RoPE: cos and sin of
+    the t, h and w axes, each (n_axis, pairs) fp32 with rows padded to a
+    multiple of 4 floats, and the channel split (d_t, d_h, d_w)."""
+    cos: Tuple[torch.Tensor, torch.Tensor, torch.Tensor]
+    sin: Tuple[torch.Tensor, torch.Tensor, torch.Tensor]
+    split: Tuple[int, int, int]
+
+
+def create_abs_rope3d_axis_freqs(t: int, h: int, w: int, head_dim: int,
+                                 rope_split: Optional[Tuple[int, int, int]] = None, base: float = 10000.0,
+                                 device=None) -> AbsRope3dAxes:
+    """The per-axis form of create_abs_rope3d_freqs, as the reference builds
+    them (`diffusion_vae.py:112-128`, `_apply_abs_rope_axis` per chunk): the t
+    rows (t, d_t/2), the h rows (h, d_h/2) and the w rows (w, d_w/2), the same
+    values that create_abs_rope3d_freqs concatenates per token. For
+    na3d_block_attention, whose kernel then reads a few rows per axis
+    instead of one table row per token and head."""
+    split = _abs_rope_split(head_dim, rope_split)
+    cos, sin = [], []
+    for n, d in zip((t, h, w), split):
+        c, s_ = _abs_rope_axis(n, d, base, device)
+        width = -(-(d // 2) // 4) * 4
+        cp = torch.zeros((n, max(width, 4)), dtype=torch.float32, device=device)
+        sp = torch.zeros_like(cp)
+        cp[:, :d // 2] = c
+        sp[:, :d // 2] = s_
+        cos.append(cp)
+        sin.append(sp)
+    return AbsRope3dAxes(tuple(cos), tuple(sin), tuple(split))
+
+
 def create_abs_rope3d_freqs(t: int, h: int, w: int, head_dim: int,
                             rope_split: Optional[Tuple[int, int, int]] = None, base: float = 10000.0,
                             device=None) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -191,19 +242,8 @@ def create_abs_rope3d_freqs(t: int, h: int, w: int, head_dim: int,
     d_w/2 by w_pos * inv_w, with inv = 1 / base^(arange(0, d, 2) / d) computed
     in float64 and stored as fp32 and the angles formed in fp32
     (`diffusion_vae.py:106-149,265-273`)."""
-    d_t, d_h, d_w = rope_split or default_rope_dim_split(head_dim)
-    if d_t + d_h + d_w != head_dim or d_t % 2 or d_h % 2 or d_w % 2:
-        raise ValueError(f"rope split {(d_t, d_h, d_w)} must be even and sum to head_dim {head_dim}")
-
-    def axis(n, d):
-        inv = 1.0 / torch.pow(torch.tensor(float(base), dtype=torch.float64),
-                              torch.arange(0, d, 2, dtype=torch.float64) / d)
-        ang = torch.arange(n, dtype=torch.float32, device=device)[:, None] * inv.to(torch.float32).to(device)[None, :]
-        return torch.cos(ang), torch.sin(ang)
-
-    ct, st = axis(t, d_t)
-    ch, sh = axis(h, d_h)
-    cw, sw = axis(w, d_w)
+    d_t, d_h, d_w = _abs_rope_split(head_dim, rope_split)
+    (ct, st), (ch, sh), (cw, sw) = (_abs_rope_axis(n, d, base, device) for n, d in ((t, d_t), (h, d_h), (w, d_w)))
 
     def grid(ft, fh, fw):
         gt = ft[:, None, None, :].expand(t, h, w, d_t // 2)
