@@ -250,19 +250,22 @@ int32_t vx_na3d_qprep_check(const void* q, const void* k, const void* v, const v
                             int64_t rope_stride);
 
 /*
- * vx_na3d_qprep_fwd with the rotation taken from per-axis tables, as the
- * reference forms it (_apply_abs_rope_axis per t, h and w chunk): with
- * rope_split = (d_t, d_h, d_w), pair j of a token (t, y, x) turns by
- *   (rope_cos_t[t*rope_strides[0] + j], rope_sin_t[...])          j < d_t/2
- *   (rope_cos_h[y*rope_strides[1] + j - d_t/2], rope_sin_h[...])   j < (d_t+d_h)/2
- *   (rope_cos_w[x*rope_strides[2] + j - (d_t+d_h)/2], ...)         otherwise
+ * vx_na3d_qprep_fwd with the rotation taken from per-axis rows, as the
+ * reference forms it (_apply_abs_rope_axis per t, h and w chunk). rope_cos
+ * and rope_sin each hold t + h + w rows of rope_stride floats: rows 0..t-1
+ * the t axis, rows t..t+h-1 the h axis, rows t+h..t+h+w-1 the w axis, each
+ * row's value for pair j at column j. With rope_split = (d_t, d_h, d_w), pair
+ * j of token (tt, y, x) turns by
+ *   (rope_cos[tt*rope_stride + j], rope_sin[...])            j < d_t/2
+ *   (rope_cos[(t + y)*rope_stride + j], ...)                 j < (d_t+d_h)/2
+ *   (rope_cos[(t + h + x)*rope_stride + j], ...)             otherwise
  * which equals vx_na3d_qprep_fwd with the per-token tables that concatenate
- * these rows (create_abs_rope3d_freqs's), bit for bit. The tables hold at
- * least t, h and w rows; each is fp32, 16-byte aligned, its stride a multiple
- * of 4 and at least its d/2 pairs; d_t, d_h, d_w even and summing to
- * head_dim, d_t and d_h multiples of 8 (the default split of head dims 64
- * and 128 is). rope_split = NULL: no rotation. A few rows per axis replace one
- * table row per token, which every head's workgroups re-read.
+ * these parts (create_abs_rope3d_freqs's), bit for bit. Tables fp32, 16-byte
+ * aligned, rope_stride a multiple of 4 and >= head_dim/2, (t+h+w)*rope_stride
+ * < 2^31; d_t, d_h, d_w even and summing to head_dim, d_t and d_h multiples
+ * of 8 (the default split of head dims 64 and 128 is). rope_split = NULL: no
+ * rotation. A few hundred rows replace one table row per token, which every
+ * head's workgroups re-read.
  *
  * Replaces the q half of src/vidax/models/ltx2_5/diffusion_vae.py:263-277
  * with _apply_abs_rope's per-axis tables (:112-149, _rope_inv_freqs :106-109).
@@ -270,18 +273,15 @@ int32_t vx_na3d_qprep_check(const void* q, const void* k, const void* v, const v
 int32_t vx_na3d_qprep_axes_fwd(const void* q, const void* k, const void* v, void* out, int32_t batch, int32_t t,
                                int32_t h, int32_t w, int32_t num_heads, int32_t head_dim, int32_t kernel_t,
                                int32_t kernel_h, int32_t kernel_w, const float* q_norm_weight, float eps,
-                               float q_post_scale, const float* rope_cos_t, const float* rope_sin_t,
-                               const float* rope_cos_h, const float* rope_sin_h, const float* rope_cos_w,
-                               const float* rope_sin_w, const int64_t* rope_strides, const int32_t* rope_split,
-                               void* stream);
+                               float q_post_scale, const float* rope_cos, const float* rope_sin, int64_t rope_stride,
+                               const int32_t* rope_split, void* stream);
 
 /* Host-only argument check for vx_na3d_qprep_axes_fwd (no GPU needed). */
 int32_t vx_na3d_qprep_axes_check(const void* q, const void* k, const void* v, const void* out, int32_t batch,
                                  int32_t t, int32_t h, int32_t w, int32_t num_heads, int32_t head_dim,
                                  int32_t kernel_t, int32_t kernel_h, int32_t kernel_w, const float* q_norm_weight,
-                                 float eps, float q_post_scale, const float* rope_cos_t, const float* rope_sin_t,
-                                 const float* rope_cos_h, const float* rope_sin_h, const float* rope_cos_w,
-                                 const float* rope_sin_w, const int64_t* rope_strides, const int32_t* rope_split);
+                                 float eps, float q_post_scale, const float* rope_cos, const float* rope_sin,
+                                 int64_t rope_stride, const int32_t* rope_split);
 
 /*
  * Fused attention prologue: RMSNorm and/or 3D rotary embedding of q or k in

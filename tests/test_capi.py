@@ -460,32 +460,30 @@ def test_na3d_qprep_check():
         assert frag in _lib.last_error(), (kw, _lib.last_error())
 
 
-def _axes_check(q=A, D=128, split=(32, 48, 48), strides=(16, 24, 24), tables=None, post=0.088):
-    L = _lib.lib()
-    tabs = tables if tables is not None else [A] * 6
+def _axes_check(q=A, D=128, split=(32, 48, 48), stride=64, cos=A, sin=A, grid=(3, 8, 80), post=0.088):
     sp = None if split is None else (ctypes.c_int32 * 3)(*split)
-    st = None if strides is None else (ctypes.c_int64 * 3)(*strides)
-    return L.vx_na3d_qprep_axes_check(q, A, A, A, 1, 3, 8, 80, 2, D, 3, 7, 7, A, ctypes.c_float(1e-6),
-                                      ctypes.c_float(post), *tabs, st, sp)
+    return _lib.lib().vx_na3d_qprep_axes_check(q, A, A, A, 1, *grid, 2, D, 3, 7, 7, A, ctypes.c_float(1e-6),
+                                               ctypes.c_float(post), cos, sin, stride, sp)
 
 
 def test_na3d_qprep_axes_check():
-    """The per-axis rope tables: split even and summing to head_dim, t and h
-    parts multiples of 8, aligned tables with strides of whole 16-byte rows."""
+    """The per-axis rope rows: split even and summing to head_dim, t and h
+    parts multiples of 8, aligned tables of whole 16-byte rows of at least
+    head_dim/2 floats, (t + h + w) rows addressable with 32-bit offsets."""
     assert _axes_check() == _lib.VX_OK
-    assert _axes_check(D=64, split=(16, 24, 24), strides=(8, 12, 12)) == _lib.VX_OK
-    assert _axes_check(split=(0, 64, 64), strides=(0, 32, 32), tables=[None, None] + [A] * 4) == _lib.VX_OK
-    assert _axes_check(split=None, strides=None, tables=[None] * 6) == _lib.VX_OK  # no rope
+    assert _axes_check(D=64, split=(16, 24, 24), stride=32) == _lib.VX_OK
+    assert _axes_check(split=(0, 64, 64), stride=68) == _lib.VX_OK
+    assert _axes_check(split=None, cos=None, sin=None) == _lib.VX_OK  # no rope
     for kw, code, frag in [
         (dict(split=(32, 48, 40)), _lib.VX_ERR_INVALID_ARGUMENT, "sum to head_dim"),
         (dict(split=(33, 47, 48)), _lib.VX_ERR_INVALID_ARGUMENT, "even"),
         (dict(split=(36, 44, 48)), _lib.VX_ERR_UNSUPPORTED, "multiples of 8"),
-        (dict(strides=(16, 22, 24)), _lib.VX_ERR_INVALID_ARGUMENT, "rope_strides[1]"),
-        (dict(strides=(12, 24, 24)), _lib.VX_ERR_INVALID_ARGUMENT, "rope_strides[0]"),
-        (dict(strides=None), _lib.VX_ERR_INVALID_ARGUMENT, "rope_strides"),
+        (dict(stride=60), _lib.VX_ERR_INVALID_ARGUMENT, "rope_stride"),
+        (dict(stride=66), _lib.VX_ERR_INVALID_ARGUMENT, "rope_stride"),
         (dict(split=None), _lib.VX_ERR_INVALID_ARGUMENT, "rope_split"),
-        (dict(tables=[A, A, A, None, A, A]), _lib.VX_ERR_INVALID_ARGUMENT, "axis 1"),
-        (dict(tables=[A, A, A, A, A + 8, A]), _lib.VX_ERR_INVALID_ARGUMENT, "aligned"),
+        (dict(sin=None), _lib.VX_ERR_INVALID_ARGUMENT, "both"),
+        (dict(cos=A + 8), _lib.VX_ERR_INVALID_ARGUMENT, "aligned"),
+        (dict(grid=(3, 8, 80), stride=(1 << 31) // 91 + 4 & ~3), _lib.VX_ERR_UNSUPPORTED, "2^31"),
         (dict(q=None), _lib.VX_ERR_INVALID_ARGUMENT, "non-NULL"),
     ]:
         assert _axes_check(**kw) == code, kw

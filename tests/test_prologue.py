@@ -193,21 +193,23 @@ def test_abs_rope_tables_equal_axis_form():
 
 
 def test_abs_rope_axis_tables_equal_token_tables():
-    """The per-axis rows the fused NA kernel reads, gathered per token, are
-    bit for bit the per-token tables (both come from one per-axis routine)."""
+    """The per-axis rows the fused NA kernel reads (t rows, then h rows, then
+    w rows, each axis in its own pair columns), gathered per token as the
+    kernel reads them, are bit for bit the per-token tables (both come from
+    one per-axis routine)."""
     from vidax_amd import create_abs_rope3d_axis_freqs, create_abs_rope3d_freqs
     for T, H, W, HD, split in [(3, 5, 7, 64, None), (2, 4, 6, 128, None), (4, 3, 5, 64, (16, 24, 24)),
-                               (2, 3, 4, 128, (0, 64, 64))]:
+                               (2, 3, 4, 128, (0, 64, 64)), (1, 2, 3, 64, (32, 32, 0))]:
         cos, sin = create_abs_rope3d_freqs(T, H, W, HD, rope_split=split)
         ax = create_abs_rope3d_axis_freqs(T, H, W, HD, rope_split=split)
-        d_t, d_h, d_w = ax.split
-        assert d_t + d_h + d_w == HD
-        for tok, tabs in ((cos, ax.cos), (sin, ax.sin)):
-            for n, tab in zip((T, H, W), tabs):
-                assert tab.shape[0] == n and tab.shape[1] % 4 == 0 and tab.dtype == torch.float32
-            gathered = torch.cat([tabs[0][:, None, None, :d_t // 2].expand(T, H, W, d_t // 2),
-                                  tabs[1][None, :, None, :d_h // 2].expand(T, H, W, d_h // 2),
-                                  tabs[2][None, None, :, :d_w // 2].expand(T, H, W, d_w // 2)], dim=-1)
+        p_t, p_h = ax.split[0] // 2, (ax.split[0] + ax.split[1]) // 2
+        assert ax.grid == (T, H, W) and sum(ax.split) == HD
+        assert ax.cos.shape == (T + H + W, -(-(HD // 2) // 4) * 4) and ax.cos.dtype == torch.float32
+        t, y, x = torch.meshgrid(torch.arange(T), torch.arange(H), torch.arange(W), indexing="ij")
+        j = torch.arange(HD // 2)
+        row = torch.where(j < p_t, t[..., None], torch.where(j < p_h, T + y[..., None], T + H + x[..., None]))
+        for tok, tab in ((cos, ax.cos), (sin, ax.sin)):
+            gathered = tab[row, j.expand_as(row)]
             assert torch.equal(gathered.reshape(tok.shape), tok)
 
 

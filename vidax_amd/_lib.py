@@ -63,7 +63,7 @@ _NA3D_ARGS = [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i
 _FLASH_BIAS_ARGS = [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64p, _i32, _i32, _i32, _i32, _i32,
                     _i64p, _i64p, _i64p, _i64p, _f32]
 _NA3D_QPREP_ARGS = [_p, _p, _p, _p] + [_i32] * 9 + [_p, _f32, _f32, _p, _p, _i64]
-_NA3D_QPREP_AXES_ARGS = [_p, _p, _p, _p] + [_i32] * 9 + [_p, _f32, _f32] + [_p] * 6 + [_i64p, _i32p]
+_NA3D_QPREP_AXES_ARGS = [_p, _p, _p, _p] + [_i32] * 9 + [_p, _f32, _f32, _p, _p, _i64, _i32p]
 _PROLOGUE_ARGS = [_p, _p, _p, _f32, _i32, _p, _p, _i64, _i32, _i32, _i32, _i32, _i64p, _i64p]
 _SCALED_PROLOGUE_ARGS = _PROLOGUE_ARGS[:5] + [_f32] + _PROLOGUE_ARGS[5:]
 

@@ -107,20 +107,19 @@ __device__ __forceinline__ void prep_q(bf16x8 (&qr)[NDS], int hf, int64_t tok, i
     }
   }
   if (rope && (a.q_prep & kQPrepRopeAxes)) {
-    // per-axis tables: the lane's 4 pairs 8 ds + 4 hf + 0..3 lie in one
-    // axis's part (its boundaries are multiples of 4); a few rows per axis,
-    // shared by every token and head, instead of one table row per token
+    // per-axis rows (t rows, then h rows, then w rows of one table): the
+    // lane's 4 pairs 8 ds + 4 hf + 0..3 lie in one axis's part (its
+    // boundaries are multiples of 4) and are read at their own columns of
+    // that axis's row; a few hundred rows shared by every token and head
+    // instead of one table row per token. 32-bit element offsets.
+    const int st = (int)a.q_tab_stride;
+    const int row_t = tq * st, row_h = (a.T + yq) * st, row_w = (a.T + a.Hs + xq) * st;
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds) {
       const int j = ds * 8 + hf * 4;
-      const bool in_t = j < a.q_ax_pairs[0], in_h = !in_t && j < a.q_ax_pairs[1];
-      const int64_t off = in_t ? tq * a.q_ax_stride[0] + j
-                               : (in_h ? yq * a.q_ax_stride[1] + (j - a.q_ax_pairs[0])
-                                       : xq * a.q_ax_stride[2] + (j - a.q_ax_pairs[1]));
-      const float* cb = in_t ? a.q_cos_ax[0] : (in_h ? a.q_cos_ax[1] : a.q_cos_ax[2]);
-      const float* sb = in_t ? a.q_sin_ax[0] : (in_h ? a.q_sin_ax[1] : a.q_sin_ax[2]);
-      cs[ds] = *(const f32x4*)(cb + off);
-      sn[ds] = *(const f32x4*)(sb + off);
+      const int off = (j < a.q_ax_pairs[0] ? row_t : (j < a.q_ax_pairs[1] ? row_h : row_w)) + j;
+      cs[ds] = *(const f32x4*)(a.q_cos + off);
+      sn[ds] = *(const f32x4*)(a.q_sin + off);
     }
   } else if (rope) {
     const float* cr = a.q_cos + tok * a.q_tab_stride + hf * 4;

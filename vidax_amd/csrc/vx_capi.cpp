@@ -398,10 +398,6 @@ int32_t na3d_check(const void* q, const void* k, const void* v, const void* out,
     args->q_eps = 0.f;
     args->q_post_scale = 1.f;
     args->q_tab_stride = 0;
-    for (int i = 0; i < 3; ++i) {
-      args->q_cos_ax[i] = args->q_sin_ax[i] = nullptr;
-      args->q_ax_stride[i] = 0;
-    }
     args->q_ax_pairs[0] = args->q_ax_pairs[1] = 0;
   }
   return ok();
@@ -438,27 +434,22 @@ int32_t na3d_qprep_check(const float* weight, float eps, float post_scale, const
     args->q_cos = rope_cos;
     args->q_sin = rope_sin;
     args->q_tab_stride = rope_stride;
-    for (int i = 0; i < 3; ++i) {
-      args->q_cos_ax[i] = args->q_sin_ax[i] = nullptr;
-      args->q_ax_stride[i] = 0;
-    }
     args->q_ax_pairs[0] = args->q_ax_pairs[1] = 0;
   }
   return VX_OK;
 }
 
-// The per-axis rotation tables of vx_na3d_qprep_axes_fwd, checked into a:
+// The per-axis rotation table of vx_na3d_qprep_axes_fwd, checked into a:
 // split (d_t, d_h, d_w) even, summing to head_dim, with d_t and d_h multiples
-// of 8 (the kernel takes a lane's 4 pairs from one axis); per axis with
-// d > 0, 16-byte aligned cos/sin rows of d/2 pairs, stride a multiple of 4.
-int32_t na3d_rope_axes_check(const float* const (&cos_ax)[3], const float* const (&sin_ax)[3],
-                             const int64_t* strides, const int32_t* split, int32_t D, vx::Na3dArgs* args) {
-  const bool any = cos_ax[0] || cos_ax[1] || cos_ax[2] || sin_ax[0] || sin_ax[1] || sin_ax[2];
+// of 8 (the kernel takes a lane's 4 pairs from one axis); 16-byte aligned
+// cos/sin tables of t + h + w rows of rope_stride >= head_dim/2 floats (a
+// multiple of 4), fewer than 2^31 elements (the kernel's offsets are 32-bit).
+int32_t na3d_rope_axes_check(const float* cos, const float* sin, int64_t stride, const int32_t* split, int32_t D,
+                             int32_t t, int32_t h, int32_t w, vx::Na3dArgs* args) {
   if (split == nullptr) {
-    if (any) return fail(VX_ERR_INVALID_ARGUMENT, "rope tables need rope_split");
+    if (cos != nullptr || sin != nullptr) return fail(VX_ERR_INVALID_ARGUMENT, "rope tables need rope_split");
     return VX_OK;
   }
-  if (strides == nullptr) return fail(VX_ERR_INVALID_ARGUMENT, "rope_strides must be given with rope_split");
   for (int i = 0; i < 3; ++i)
     if (split[i] < 0 || split[i] % 2 != 0)
       return fail(VX_ERR_INVALID_ARGUMENT, "rope_split[%d] = %d must be even and >= 0", i, split[i]);
@@ -468,23 +459,21 @@ int32_t na3d_rope_axes_check(const float* const (&cos_ax)[3], const float* const
   if (split[0] % 8 != 0 || split[1] % 8 != 0)
     return fail(VX_ERR_UNSUPPORTED, "rope_split (%d, %d, %d): the t and h parts must be multiples of 8", split[0],
                 split[1], split[2]);
-  for (int i = 0; i < 3; ++i) {
-    if (split[i] == 0) continue;
-    if (cos_ax[i] == nullptr || sin_ax[i] == nullptr)
-      return fail(VX_ERR_INVALID_ARGUMENT, "axis %d has %d rotated channels but no cos/sin table", i, split[i]);
-    if (!aligned16(cos_ax[i]) || !aligned16(sin_ax[i]))
-      return fail(VX_ERR_INVALID_ARGUMENT, "the axis %d cos/sin tables must be 16-byte aligned", i);
-    if (strides[i] < split[i] / 2 || strides[i] % 4 != 0)
-      return fail(VX_ERR_INVALID_ARGUMENT, "rope_strides[%d] (%lld) must be a multiple of 4 and >= %d", i,
-                  (long long)strides[i], split[i] / 2);
-  }
+  if (cos == nullptr || sin == nullptr)
+    return fail(VX_ERR_INVALID_ARGUMENT, "rope_split given without both rope_cos and rope_sin");
+  if (!aligned16(cos) || !aligned16(sin))
+    return fail(VX_ERR_INVALID_ARGUMENT, "rope_cos and rope_sin must be 16-byte aligned");
+  if (stride < D / 2 || stride % 4 != 0)
+    return fail(VX_ERR_INVALID_ARGUMENT, "rope_stride (%lld) must be a multiple of 4 and >= head_dim/2 = %d",
+                (long long)stride, D / 2);
+  if (((int64_t)t + h + w) * stride >= ((int64_t)1 << 31))
+    return fail(VX_ERR_UNSUPPORTED, "rope tables of %lld rows x %lld floats exceed 2^31 elements",
+                (long long)t + h + w, (long long)stride);
   if (args != nullptr) {
     args->q_prep |= vx::kQPrepRope | vx::kQPrepRopeAxes;
-    for (int i = 0; i < 3; ++i) {
-      args->q_cos_ax[i] = cos_ax[i];
-      args->q_sin_ax[i] = sin_ax[i];
-      args->q_ax_stride[i] = strides[i];
-    }
+    args->q_cos = cos;
+    args->q_sin = sin;
+    args->q_tab_stride = stride;
     args->q_ax_pairs[0] = split[0] / 2;
     args->q_ax_pairs[1] = (split[0] + split[1]) / 2;
   }
@@ -822,36 +811,31 @@ int32_t vx_na3d_qprep_fwd(const void* q, const void* k, const void* v, void* out
 int32_t vx_na3d_qprep_axes_check(const void* q, const void* k, const void* v, const void* out, int32_t batch,
                                  int32_t t, int32_t h, int32_t w, int32_t num_heads, int32_t head_dim,
                                  int32_t kernel_t, int32_t kernel_h, int32_t kernel_w, const float* q_norm_weight,
-                                 float eps, float q_post_scale, const float* rope_cos_t, const float* rope_sin_t,
-                                 const float* rope_cos_h, const float* rope_sin_h, const float* rope_cos_w,
-                                 const float* rope_sin_w, const int64_t* rope_strides, const int32_t* rope_split) {
+                                 float eps, float q_post_scale, const float* rope_cos, const float* rope_sin,
+                                 int64_t rope_stride, const int32_t* rope_split) {
   int32_t rc = na3d_check(q, k, v, out, batch, t, h, w, num_heads, head_dim, kernel_t, kernel_h, kernel_w, 1.0f,
                           nullptr);
   if (rc != VX_OK) return rc;
   if ((rc = na3d_qprep_check(q_norm_weight, eps, q_post_scale, nullptr, nullptr, 0, head_dim, nullptr)) != VX_OK)
     return rc;
-  const float* const cs[3] = {rope_cos_t, rope_cos_h, rope_cos_w};
-  const float* const sn[3] = {rope_sin_t, rope_sin_h, rope_sin_w};
-  if ((rc = na3d_rope_axes_check(cs, sn, rope_strides, rope_split, head_dim, nullptr)) != VX_OK) return rc;
+  if ((rc = na3d_rope_axes_check(rope_cos, rope_sin, rope_stride, rope_split, head_dim, t, h, w, nullptr)) != VX_OK)
+    return rc;
   return ok();
 }
 
 int32_t vx_na3d_qprep_axes_fwd(const void* q, const void* k, const void* v, void* out, int32_t batch, int32_t t,
                                int32_t h, int32_t w, int32_t num_heads, int32_t head_dim, int32_t kernel_t,
                                int32_t kernel_h, int32_t kernel_w, const float* q_norm_weight, float eps,
-                               float q_post_scale, const float* rope_cos_t, const float* rope_sin_t,
-                               const float* rope_cos_h, const float* rope_sin_h, const float* rope_cos_w,
-                               const float* rope_sin_w, const int64_t* rope_strides, const int32_t* rope_split,
-                               void* stream) {
+                               float q_post_scale, const float* rope_cos, const float* rope_sin, int64_t rope_stride,
+                               const int32_t* rope_split, void* stream) {
   vx::Na3dArgs args;
   int32_t rc = na3d_check(q, k, v, out, batch, t, h, w, num_heads, head_dim, kernel_t, kernel_h, kernel_w, 1.0f,
                           &args);
   if (rc != VX_OK) return rc;
   if ((rc = na3d_qprep_check(q_norm_weight, eps, q_post_scale, nullptr, nullptr, 0, head_dim, &args)) != VX_OK)
     return rc;
-  const float* const cs[3] = {rope_cos_t, rope_cos_h, rope_cos_w};
-  const float* const sn[3] = {rope_sin_t, rope_sin_h, rope_sin_w};
-  if ((rc = na3d_rope_axes_check(cs, sn, rope_strides, rope_split, head_dim, &args)) != VX_OK) return rc;
+  if ((rc = na3d_rope_axes_check(rope_cos, rope_sin, rope_stride, rope_split, head_dim, t, h, w, &args)) != VX_OK)
+    return rc;
   if ((rc = injected()) != VX_OK) return rc;
   const char* launched = "";
   const int err = vx::launch_na3d_fwd(args, stream, &launched);

@@ -75,14 +75,11 @@ struct Na3dArgs {
   const float* q_cos;
   const float* q_sin;
   int64_t q_tab_stride;
-  // bit 8 (with 4): the rotation from per-axis tables instead: pair j <
-  // q_ax_pairs[0] by (q_cos_ax[0], q_sin_ax[0]) at row t (q_ax_stride[0]
-  // apart), j < q_ax_pairs[1] by axis 1 at row y (column j - q_ax_pairs[0]),
-  // the rest by axis 2 at row x (column j - q_ax_pairs[1]); the boundaries
-  // are multiples of 4
-  const float* q_cos_ax[3];
-  const float* q_sin_ax[3];
-  int64_t q_ax_stride[3];
+  // bit 8 (with 4): q_cos / q_sin hold per-axis rows instead, T rows of the
+  // t axis, then Hs of the h axis, then W of the w axis (q_tab_stride
+  // apart, fewer than 2^31 elements): pair j < q_ax_pairs[0] of token
+  // (t, y, x) is read at column j of row t, j < q_ax_pairs[1] of row T + y,
+  // the rest of row T + Hs + x; the boundaries are multiples of 4
   int32_t q_ax_pairs[2];
 };
 constexpr int32_t kQPrepNorm = 1, kQPrepScale = 2, kQPrepRope = 4, kQPrepRopeAxes = 8;

@@ -135,23 +135,22 @@ def na3d_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         from .prologue import _tables
         cos_t, sin_t, stride = _tables(freqs, T * H * W, HD // 2, q.device)
     if axes:
-        # per-axis tables: (n_axis, >= d/2) fp32 rows of at least T, H and W
-        # positions, 16-byte aligned, row strides a multiple of 4 floats
-        ax_c, ax_s = [], []
-        for c, s_, n, d in zip(freqs.cos, freqs.sin, (T, H, W), freqs.split):
-            for tab in (c, s_):
-                if (tab.dim() != 2 or tab.shape[0] < n or tab.shape[1] < d // 2 or tab.dtype != torch.float32
-                        or tab.device != q.device):
-                    raise ValueError(f"per-axis rope table {tuple(tab.shape)} does not cover {n} positions "
-                                     f"x {d // 2} pairs (fp32, on q's device)")
-            ax_c.append(c if (c.stride(1) == 1 and c.stride(0) % 4 == 0 and c.data_ptr() % 16 == 0)
-                        else _pad_rows(c))
-            ax_s.append(s_ if (s_.stride(1) == 1 and s_.stride(0) % 4 == 0 and s_.data_ptr() % 16 == 0)
-                        else _pad_rows(s_))
-        ax_strides = (ctypes.c_int64 * 3)(*[int(c.stride(0)) for c in ax_c])
-        for c, s_ in zip(ax_c, ax_s):
-            if s_.stride(0) != c.stride(0):
-                raise ValueError("the cos and sin tables of an axis must have the same row stride")
+        # one fp32 table each of T + H + W rows (t axis, h axis, w axis)
+        if tuple(freqs.grid) != (T, H, W):
+            raise ValueError(f"per-axis rope rows built for the grid {tuple(freqs.grid)}, not {(T, H, W)}")
+        for tab in (freqs.cos, freqs.sin):
+            if (tab.dim() != 2 or tab.shape[0] != T + H + W or tab.shape[1] < HD // 2
+                    or tab.dtype != torch.float32 or tab.device != q.device):
+                raise ValueError(f"per-axis rope table {tuple(tab.shape)} is not ({T + H + W}, >= {HD // 2}) "
+                                 "fp32 on q's device")
+        # rows 16-byte aligned and the same stride in both tables
+        ax_c, ax_s = freqs.cos, freqs.sin
+        if not (ax_c.stride(1) == 1 and ax_c.stride(0) % 4 == 0 and ax_c.data_ptr() % 16 == 0):
+            ax_c = _pad_rows(ax_c)
+        if not (ax_s.stride(1) == 1 and ax_s.stride(0) == ax_c.stride(0) and ax_s.data_ptr() % 16 == 0):
+            ax_s = _pad_rows(ax_s)
+        if ax_s.stride(0) != ax_c.stride(0):
+            ax_c = _pad_rows(ax_c)
         ax_split = (ctypes.c_int32 * 3)(*[int(d) for d in freqs.split])
     if out is None:
         out = torch.empty_like(q)
@@ -166,8 +165,7 @@ def na3d_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                 B, T, H, W, NH, HD, int(kernel_size[0]), int(kernel_size[1]), int(kernel_size[2]),
                 weight.data_ptr() if weight is not None else None, ctypes.c_float(eps),
                 ctypes.c_float(q_post_scale),
-                ax_c[0].data_ptr(), ax_s[0].data_ptr(), ax_c[1].data_ptr(), ax_s[1].data_ptr(),
-                ax_c[2].data_ptr(), ax_s[2].data_ptr(), ax_strides, ax_split, ctypes.c_void_p(stream))
+                ax_c.data_ptr(), ax_s.data_ptr(), int(ax_c.stride(0)), ax_split, ctypes.c_void_p(stream))
         else:
             rc = _lib.lib().vx_na3d_qprep_fwd(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),

@@ -202,11 +202,15 @@ def _abs_rope_axis(n: int, d: int, base: float, device) -> Tuple[torch.Tensor, t
 
 
 class AbsRope3dAxes(NamedTuple):
-    """Per-axis tables of the absolute interleaved-pair RoPE: cos and sin of
-    the t, h and w axes, each (n_axis, pairs) fp32 with rows padded to a
-    multiple of 4 floats, and the channel split (d_t, d_h, d_w)."""
-    cos: Tuple[torch.Tensor, torch.Tensor, torch.Tensor]
-    sin: Tuple[torch.Tensor, torch.Tensor, torch.Tensor]
+    """Per-axis rows of the absolute interleaved-pair RoPE of a (t, h, w) grid:
+    cos and sin, each (t + h + w, stride) fp32 (stride = head_dim/2 rounded up
+    to 4 floats): rows 0..t-1 hold the t axis's angles in the t pairs'
+    columns, the next h rows the h axis's in the h columns, the last w rows
+    the w axis's in the w columns (other columns zero); `grid` = (t, h, w),
+    `split` = (d_t, d_h, d_w)."""
+    cos: torch.Tensor
+    sin: torch.Tensor
+    grid: Tuple[int, int, int]
     split: Tuple[int, int, int]
 
 
@@ -214,23 +218,22 @@ def create_abs_rope3d_axis_freqs(t: int, h: int, w: int, head_dim: int,
                                  rope_split: Optional[Tuple[int, int, int]] = None, base: float = 10000.0,
                                  device=None) -> AbsRope3dAxes:
     """The per-axis form of create_abs_rope3d_freqs, as the reference builds
-    them (`diffusion_vae.py:112-128`, `_apply_abs_rope_axis` per chunk): the t
-    rows (t, d_t/2), the h rows (h, d_h/2) and the w rows (w, d_w/2), the same
-    values that create_abs_rope3d_freqs concatenates per token. For
-    na3d_block_attention, whose kernel then reads a few rows per axis
-    instead of one table row per token and head."""
+    it (`diffusion_vae.py:112-128`, `_apply_abs_rope_axis` per chunk): the t,
+    h and w rows of the same values that create_abs_rope3d_freqs concatenates
+    per token, in one table. For na3d_block_attention, whose kernel then reads
+    a few hundred rows instead of one table row per token and head."""
     split = _abs_rope_split(head_dim, rope_split)
-    cos, sin = [], []
+    width = -(-(head_dim // 2) // 4) * 4
+    cos = torch.zeros((t + h + w, width), dtype=torch.float32, device=device)
+    sin = torch.zeros_like(cos)
+    row, col = 0, 0
     for n, d in zip((t, h, w), split):
         c, s_ = _abs_rope_axis(n, d, base, device)
-        width = -(-(d // 2) // 4) * 4
-        cp = torch.zeros((n, max(width, 4)), dtype=torch.float32, device=device)
-        sp = torch.zeros_like(cp)
-        cp[:, :d // 2] = c
-        sp[:, :d // 2] = s_
-        cos.append(cp)
-        sin.append(sp)
-    return AbsRope3dAxes(tuple(cos), tuple(sin), tuple(split))
+        cos[row:row + n, col:col + d // 2] = c
+        sin[row:row + n, col:col + d // 2] = s_
+        row += n
+        col += d // 2
+    return AbsRope3dAxes(cos, sin, (t, h, w), tuple(split))
 
 
 def create_abs_rope3d_freqs(t: int, h: int, w: int, head_dim: int,
