@@ -381,8 +381,8 @@ int32_t vx_flash_attn_plan(int32_t batch, int32_t seq_q, int32_t seq_k, int32_t 
 /*
  * Launch plan of vx_na3d_fwd (host only): the name of the kernel chosen by
  * the clamped x window (at head dim 64 also by the grid's h and w, which
- * decide the brick shape, and by the clamped t window min(kernel_t, t), which
- * decides the brick depth), e.g. "na3d_pipe_kernel<16, 128>", written as by
+ * decide the brick shape; and by the clamped t window min(kernel_t, t), which
+ * decides the brick depth), e.g. "na3d_tstack_kernel<128>", written as by
  * vx_flash_attn_plan. Fails as vx_na3d_check would for the same sizes.
  * Part of the replacement of src/vidax/models/ltx2_5/diffusion_vae.py:179-234.
  */

@@ -305,6 +305,11 @@ def test_na3d_kernel_name_follows_the_launch_rule():
     assert na3d_kernel_name(40, 7, 64, height=22) == "na3d_tall_kernel<64>"    # 24x48 vs 24x64
     assert na3d_kernel_name(20, 7, 64, height=11) == "na3d_pipe_kernel<16, 64>"  # 16x32 vs 12x32
     assert na3d_kernel_name(80, 7, 128, height=45) == "na3d_pipe_kernel<16, 128>"
+    # head dim 128, kw' <= 9: two t planes per brick when the t window spans 2 or more
+    assert na3d_kernel_name(80, 7, 128, height=45, depth=21, kernel_t=3) == "na3d_tstack_kernel<128>"
+    assert na3d_kernel_name(80, 7, 128, depth=2, kernel_t=5) == "na3d_tstack_kernel<128>"    # kt' = 2
+    assert na3d_kernel_name(80, 7, 128, depth=21, kernel_t=1) == "na3d_pipe_kernel<16, 128>"
+    assert na3d_kernel_name(80, 7, 64, height=45, depth=21, kernel_t=3) == "na3d_tall_kernel<64>"
     assert na3d_kernel_name(80, 11, 64) == "na3d_tall_kernel<64>"        # 80 = 5 x 16, 96 in 32-wide bricks
     assert na3d_kernel_name(160, 11, 64) == "na3d_tall_wide_kernel<64>"  # 160 = 5 x 32
     assert na3d_kernel_name(104, 11, 64) == "na3d_tall_kernel<64>"       # 112 vs 128 columns

@@ -69,6 +69,8 @@ def _na_rule(T, H, W, D, kt, kw):
     if k <= 9:
         if D == 64 and up(H, 8) * up(W, 16) <= up(H, 4) * up(W, 32):
             return "na3d_tall_kernel<64>"
+        if D == 128 and t >= 2:
+            return "na3d_tstack_kernel<128>"
         return f"na3d_pipe_kernel<16, {D}>"
     if k <= 13:
         if D == 64 and up(W, 32) == up(W, 16):

@@ -64,6 +64,9 @@ def _expected_kernel(H, W, kw, D, T=1, kt=1):
         # plane than the 1 x 4 x 32 ones
         if D == 64 and -(-H // 8) * 8 * (-(-W // 16) * 16) <= -(-H // 4) * 4 * (-(-W // 32) * 32):
             return "na3d_tall_kernel<64>"
+        # head dim 128 with a t window of 2 or more: bricks two t planes deep
+        if D == 128 and min(kt, T) >= 2:
+            return "na3d_tstack_kernel<128>"
         return f"na3d_pipe_kernel<16, {D}>"
     if k <= 13:
         # head dim 64: 32-wide bricks unless they leave more ragged columns
@@ -178,7 +181,7 @@ def test_na3d_row_offsets(gpu, shift, D, H, W):
     q[:, :, :, ::2, :, 0] = shift
     q[:, :, :, 1::2, :, 0] = 0.0
     out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), (3, 7, 7))
-    assert _lib.last_launch() == _expected_kernel(H, W, 7, D), _lib.last_launch()
+    assert _lib.last_launch() == _expected_kernel(H, W, 7, D, T, 3), _lib.last_launch()
     torch.cuda.synchronize()
     _check(out.float().cpu().numpy(), O.na3d(q, k, v, (3, 7, 7)), "oracle")
 
@@ -227,7 +230,7 @@ def test_na3d_config4_whole_grid(gpu):
     q, k, v = O.make_na3d_inputs(B, T, H, W, NH, 128, 3)
     out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), (3, 7, 7))
     from vidax_amd import _lib
-    assert _lib.last_launch() == "na3d_pipe_kernel<16, 128>", _lib.last_launch()
+    assert _lib.last_launch() == "na3d_tstack_kernel<128>", _lib.last_launch()
     o = out.float().cpu().numpy()
     ref = O.na3d_dense(q, k, v, (3, 7, 7), acc=np.float32)
     _check(o, ref, "c4 whole grid")
@@ -277,7 +280,7 @@ def test_na3d_wide_window_sampled_rows(gpu):
     B, T, H, W, NH = 1, 21, 45, 80, 24
     q, k, v = O.make_na3d_inputs(B, T, H, W, NH, 128, 6)
     out = neighborhood_attention_3d(_t(q, gpu), _t(k, gpu), _t(v, gpu), (3, 7, 31))
-    assert _lib.last_launch() == _expected_kernel(H, W, 31, 128), _lib.last_launch()
+    assert _lib.last_launch() == _expected_kernel(H, W, 31, 128, T, 3), _lib.last_launch()
     o = out.float().cpu().numpy()
     rows = [(0, 0), (20, 44), (10, 3), (10, 4), (7, 41), (13, 22)]
     ref = O.na3d(q, k, v, (3, 7, 31), ty_rows=rows)

@@ -11,6 +11,12 @@
 //   queries need, 32 keys per step, and runs the flash kernel's software
 //   pipeline (QK^T of the next chunk and PV of the previous one interleaved
 //   with the masking and lazy-rescale softmax of the current one).
+//   na3d_tstack_kernel<128> (kw' <= 9 with t windows of 2 and more, head dim
+//   128) runs the same body on 2 x 4 x 16 bricks, two 4 x 8 waves per t
+//   plane sharing one stream of kt' + 1 planes of 24-key rows (30 % fewer
+//   copied rows per query at a (3,7,7) window, no half-empty brick at
+//   widths of a multiple of 16); a wave whose t window misses the chunks
+//   around a step only copies.
 // - na3d_tall_kernel<D> (9 < kw' <= 13, and kw' <= 9 at head dim 64 when
 //   its bricks pad the grid no more): the same body on 1 x 8 x 16 bricks
 //   with waves of 8 y x 4 x queries, so that a wave's x window still fits a
@@ -404,21 +410,30 @@ void na3d_wave_kernel(const Na3dArgs a, int n_yb, int n_xb, int n_xg) {
 // 4 y x 4 x queries: for a t window of kt' planes the union of a wave's
 // windows is (kt' + 1) x (kh' + 3) rows instead of kt' x (kh' + 7), e.g. 12 x
 // 14 against 11 x 18 rows at (11, 11, 11).
-template <int SEG, int D, bool TALL = false, bool WIDE = false, bool DEEP = false>
+// TSTACK: 2 (t) x 4 (y) x 16 (x) bricks whose four 4 y x 8 x waves sit two
+// per t plane: one stream of (kt' + 1) planes serves both planes' waves, each
+// scoring only the chunks of its own kt' planes (a wave none of whose rows
+// in the previous, current and next chunk lies in its t window only copies).
+template <int SEG, int D, bool TALL = false, bool WIDE = false, bool DEEP = false, bool TSTACK = false>
 struct PipeCfg {
   static_assert(!TALL || SEG == 16, "the tall geometry reads 16-key segments");
   static_assert(!WIDE || TALL, "wide bricks are tall bricks");
   static_assert(!DEEP || WIDE, "deep bricks are wide bricks");
+  static_assert(!TSTACK || (!TALL && SEG == 16), "t-stacked bricks hold 1 x 4 x 8 waves on 16-key segments");
+  static constexpr bool kTStack = TSTACK;
   static constexpr int kWaves = WIDE ? 8 : 4;
   static constexpr int kThreads = kWaves * 64;
-  static constexpr int kQT = DEEP ? 2 : 1;               // t planes per brick (and per wave)
-  static constexpr int kBrickY = TALL ? (DEEP ? 4 : 8) : 4, kBrickX = TALL ? (WIDE ? 32 : 16) : 32;
-  static constexpr int kQX = kBrickX / kWaves;           // x columns per wave
-  static constexpr int kQY = 32 / (kQX * kQT);           // y rows per wave (and per brick)
+  static constexpr int kQT = DEEP || TSTACK ? 2 : 1;     // t planes per brick
+  static constexpr int kWT = DEEP ? 2 : 1;               // t planes per wave
+  static constexpr int kWX = TSTACK ? kWaves / 2 : kWaves;  // waves side by side in x
+  static constexpr int kBrickY = TALL ? (DEEP ? 4 : 8) : 4;
+  static constexpr int kBrickX = TALL ? (WIDE ? 32 : 16) : (TSTACK ? 16 : 32);
+  static constexpr int kQX = kBrickX / kWX;              // x columns per wave
+  static constexpr int kQY = 32 / (kQX * kWT);           // y rows per wave (and per brick)
   static constexpr int kRB = D * 2;                      // bytes of one key
   static constexpr int kRows = SEG == 16 ? 2 : 1;        // key rows per step
   // key slots per LDS row (>= kBrickX - kQX + SEG, a multiple of 8)
-  static constexpr int kNS = TALL ? (WIDE ? 48 : 32) : (SEG == 16 ? 40 : 64);
+  static constexpr int kNS = TALL ? (WIDE ? 48 : 32) : (TSTACK ? 24 : (SEG == 16 ? 40 : 64));
   // An LDS key row is D/64 half-planes of kNS slots x 128 bytes (d 0-63,
   // then d 64-127); one 1 KiB DMA copy fills 8 slots of one half-plane.
   static constexpr int kHalfL = kNS * 128;               // one half-plane of a row
@@ -438,10 +453,10 @@ struct PipeCfg {
   static_assert(kNS % kKeysPerCopy == 0 && kHalfL % 256 == 0, "whole copies per row, bank-aligned planes");
 };
 
-template <int SEG, int D, bool TALL, bool WIDE = false, bool DEEP = false>
+template <int SEG, int D, bool TALL, bool WIDE = false, bool DEEP = false, bool TSTACK = false>
 __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int n_xb) {
-  using C = PipeCfg<SEG, D, TALL, WIDE, DEEP>;
-  static_assert(C::kQY == C::kBrickY, "the waves of a brick sit side by side in x");
+  using C = PipeCfg<SEG, D, TALL, WIDE, DEEP, TSTACK>;
+  static_assert(C::kQY == C::kBrickY, "the waves of a t plane sit side by side in x");
   static_assert(C::kBrickX - C::kQX + SEG <= C::kNS, "a wave's segment stays inside the LDS row");
   __shared__ __attribute__((aligned(16))) unsigned char smem[C::kSmem];
   VX_LDS unsigned char* const lds = (VX_LDS unsigned char*)smem;
@@ -502,14 +517,16 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   const int nrows = NT * NY;
   const int n_steps = (nrows + C::kRows - 1) / C::kRows;
 
-  // ---- this wave's queries: t planes t..t+kQT-1, y rows y0..y0+kBrickY-1,
-  // x columns xq0..xq0+kQX-1.
-  const int xq0 = x0 + C::kQX * wave;
+  // ---- this wave's queries: t planes tw..tw+kWT-1 (tw = t, or t + 1 for the
+  // second pair of t-stacked waves), y rows y0..y0+kBrickY-1, x columns
+  // xq0..xq0+kQX-1.
+  const int tw = t + wave / C::kWX;
+  const int xq0 = x0 + C::kQX * (wave % C::kWX);
   const int ox = uni(window_start(min(xq0, W - 1), W, kw) - X_lo);  // wave's first x slot, <= kBrickX - kQX
 
   // ---- this lane's query and its window.
-  const int tq = t + col / (C::kQX * C::kQY), yq = y0 + col / C::kQX % C::kQY, xq = xq0 + col % C::kQX;
-  const bool wave_in = y0 < Hs && xq0 < W;  // wave-uniform: some query of the wave is in the grid
+  const int tq = tw + col / (C::kQX * C::kQY), yq = y0 + col / C::kQX % C::kQY, xq = xq0 + col % C::kQX;
+  const bool wave_in = y0 < Hs && xq0 < W && tw < T;  // wave-uniform: some query of the wave is in the grid
   const int tqc = min(tq, T - 1), yqc = min(yq, Hs - 1), xqc = min(xq, W - 1);
   const int sy = window_start(yqc, Hs, kh) - Y_lo;
   const int st = window_start(tqc, T, kt) - t_lo;  // (deep bricks: the lane's first plane in the box)
@@ -725,9 +742,22 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
   // rr: the rows of step s on entry (their K was issued two steps ago), the
   // rows of step s + 2 on return. IN (compile-time, so that the loop carries
   // no per-step test of it): some query of this wave lies inside the grid.
+  // t-stacked bricks: whether some row of chunk c (rows r) lies in this
+  // wave's t window (st is the wave's first plane in the box: its lanes
+  // share one t plane)
+  const int st_w = C::kTStack ? uni(st) : 0;
+  auto chunk_active = [&](const StepRows& r, int c) -> bool {
+    if constexpr (!C::kTStack) return true;
+    const int r0 = c * C::kRows;
+    return (r0 < nrows && (unsigned)(r.tr0 - st_w) < (unsigned)kt) ||
+           (r0 + 1 < nrows && (unsigned)(r.tr1 - st_w) < (unsigned)kt);
+  };
   auto step = [&](auto in_tag, const int s, f32x16& S, f32x16& Sn, const bf16x8 (&Pp)[2], bf16x8 (&P)[2],
-                  StepRows& rr) __attribute__((always_inline)) {
+                  StepRows& rr, const StepRows& rn, bool& act_prev) __attribute__((always_inline)) {
     constexpr bool IN = decltype(in_tag)::value;
+    // (t-stacked bricks) chunk s's rows are rr's on entry, chunk s+1's rn's
+    const bool act_cur = chunk_active(rr, s), act_next = chunk_active(rn, s + 1);
+    const bool idle = C::kTStack && !act_prev && !act_cur && !act_next;
     // The previous step's copies (K of s+1, V of s-1) have landed once this
     // wave has none outstanding; the barrier publishes everyone's and frees
     // K slot s%2 (K of s, read last step) and V slot s%2 (V of s-2).
@@ -765,13 +795,17 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
     // (IN is the tag's value; the 1 x 4 x 32 bricks pass the runtime flag
     // instead, one loop for all waves: their two loops measured ~1 % slower
     // at the (3,7,7) config, whose x edge holds waves without queries)
-    if (!(IN && (TALL || wave_in))) {
-      // no query of this wave is inside the grid (the ragged x or y edge):
-      // it only copies its share of the rows
+    if (!(IN && (TALL || wave_in)) || idle) {
+      // no query of this wave is inside the grid (the ragged x or y edge),
+      // or (t-stacked bricks) none of chunks s-1, s, s+1 has a row in its t
+      // window: it only copies its share of the rows. An idle step's chunk
+      // s+1 scores start from the x window alone (no row of it counts).
 #pragma unroll
       for (int j = 0; j < kStepCopies; ++j) copy(j);
       P[0] = bf16x8{};
       P[1] = bf16x8{};
+      if (idle) Sn = s_init;
+      act_prev = act_cur;
       return;
     }
     // PV fragment f < kPV: key half j = f / kDB, d block f % kDB; then QK^T.
@@ -907,20 +941,22 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
       }
     }
     l_run += l_tile;
+    act_prev = act_cur;
   };
 
   f32x16 S2;
   bf16x8 P2[2];
   // the key loop; the tall bricks run one copy for the waves with queries
   // and one for the others
+  bool act_prev = false;  // chunk -1 (none)
   auto key_loop = [&](auto in_tag) __attribute__((always_inline)) {
     int s = 0;
     for (; s + 1 < n_steps; s += 2) {
-      step(in_tag, s, S, S2, Pp, P2, rows_even);
-      step(in_tag, s + 1, S2, S, P2, Pp, rows_odd);
+      step(in_tag, s, S, S2, Pp, P2, rows_even, rows_odd, act_prev);
+      step(in_tag, s + 1, S2, S, P2, Pp, rows_odd, rows_even, act_prev);
     }
     if (s < n_steps) {
-      step(in_tag, s, S, S2, Pp, P2, rows_even);
+      step(in_tag, s, S, S2, Pp, P2, rows_even, rows_odd, act_prev);
       Pp[0] = P2[0];
       Pp[1] = P2[1];
     }
@@ -940,7 +976,7 @@ __device__ __forceinline__ void na3d_pipe_body(const Na3dArgs& a, int n_yb, int 
 
   const float lt = halves_sum(l_run);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-  store_na_rows<kDB, C::kQX, C::kQY>(O, inv, og, tok_stride, t, y0, xq0, T, Hs, W, lane);
+  store_na_rows<kDB, C::kQX, C::kQY>(O, inv, og, tok_stride, tw, y0, xq0, T, Hs, W, lane);
 }
 
 // Three waves per SIMD for the 32-key segments at head dim 64 (146 VGPRs,
@@ -980,6 +1016,14 @@ void na3d_deep_kernel(const Na3dArgs a, int n_yb, int n_xb) {
   na3d_pipe_body<16, D, true, true, true>(a, n_yb, n_xb);
 }
 
+// Head dim 128, windows up to 9 wide and t windows of 2 and more: the
+// t-stacked 2 x 4 x 16 bricks, two workgroups of 48 KiB per CU.
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void na3d_tstack_kernel(const Na3dArgs a, int n_yb, int n_xb) {
+  na3d_pipe_body<16, D, false, false, false, true>(a, n_yb, n_xb);
+}
+
 }  // namespace
 
 int launch_na3d_fwd(const Na3dArgs& a, void* stream, const char** launched) {
@@ -1015,6 +1059,15 @@ int launch_na3d_fwd(const Na3dArgs& a, void* stream, const char** launched) {
       dim3 grid((unsigned)((a.T + 1) / 2) * n_yb * n_xb, a.NH, a.B);
       hipLaunchKernelGGL((na3d_deep_kernel<64>), grid, dim3(512), 0, st, a, n_yb, n_xb);
       *launched = "na3d_deep_kernel<64>";
+      return (int)hipGetLastError();
+    }
+    case kNaTStack: {
+      if (a.D != 128) return (int)hipErrorNotSupported;
+      const int n_yb = (a.Hs + 3) / 4;
+      const int n_xb = (a.W + 15) / 16;
+      dim3 grid((unsigned)((a.T + 1) / 2) * n_yb * n_xb, a.NH, a.B);
+      hipLaunchKernelGGL((na3d_tstack_kernel<128>), grid, dim3(256), 0, st, a, n_yb, n_xb);
+      *launched = "na3d_tstack_kernel<128>";
       return (int)hipGetLastError();
     }
     case kNaPipe16:

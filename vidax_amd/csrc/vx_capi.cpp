@@ -232,7 +232,8 @@ int32_t na3d_variant(int32_t kt_clamped, int32_t kw_clamped, int32_t D, int32_t 
   if (kw_clamped <= 9) {
     const int64_t tall_area = (int64_t)((Hs + 7) / 8 * 8) * ((W + 15) / 16 * 16);
     const int64_t pipe_area = (int64_t)((Hs + 3) / 4 * 4) * ((W + 31) / 32 * 32);
-    return D == 64 && tall_area <= pipe_area ? vx::kNaTall : vx::kNaPipe16;
+    if (D == 64) return tall_area <= pipe_area ? vx::kNaTall : vx::kNaPipe16;
+    return kt_clamped >= vx::kNaTStackMinKt ? vx::kNaTStack : vx::kNaPipe16;
   }
   if (kw_clamped <= 13) {
     if (D != 64 || (W + 31) / 32 * 32 != (W + 15) / 16 * 16) return vx::kNaTall;
@@ -248,6 +249,7 @@ const char* na3d_kernel_label(int32_t variant, int32_t D) {
     case vx::kNaTall: return D == 64 ? "na3d_tall_kernel<64>" : "na3d_tall_kernel<128>";
     case vx::kNaTallWide: return "na3d_tall_wide_kernel<64>";
     case vx::kNaDeep: return "na3d_deep_kernel<64>";
+    case vx::kNaTStack: return "na3d_tstack_kernel<128>";
     case vx::kNaPipe32: return D == 64 ? "na3d_pipe_kernel<32, 64>" : "na3d_pipe_kernel<32, 128>";
     default: return D == 64 ? "na3d_wave_kernel<64>" : "na3d_wave_kernel<128>";
   }

@@ -92,7 +92,10 @@ enum Na3dVariant : int32_t {
   kNaWave = 3,    // 25 < kw' <= 57, head dim 128: per-wave bricks
   kNaTallWide = 4,  // head dim 64, 9 < kw' <= 13, round_up(W, 32) == round_up(W, 16): 1 x 8 x 32 bricks
   kNaDeep = 5,      // as kNaTallWide with kt' >= kNaDeepMinKt: 2 x 4 x 32 bricks
+  kNaTStack = 6,    // as kNaPipe16 at head dim 128 with kt' >= kNaTStackMinKt: 2 x 4 x 16 bricks
 };
+// t windows (clamped) from which the plan takes the t-stacked bricks
+constexpr int32_t kNaTStackMinKt = 2;
 // t windows (clamped) from which the plan takes the deep bricks
 constexpr int32_t kNaDeepMinKt = 5;
 

@@ -22,13 +22,15 @@ def na3d_kernel_name(width: int, kernel_w: int, head_dim: int = 128, height: Opt
     """Name of the kernel the library launches for this x window (the C ABI's
     launch plan): row streaming with 16-key x segments up to kw' = 9 (at head
     dim 64 the tall bricks instead when they pad the height x width plane no
-    more), its tall-brick form up to kw' = 13 (at head dim 64 in 32-wide
+    more; at head dim 128 bricks of two t planes when kt' >= 2), its
+    tall-brick form up to kw' = 13 (at head dim 64 in 32-wide
     bricks when the width rounds up to the same multiple of 16 and 32, two t
     planes deep for t windows kt' = min(kernel_t, depth) of 5 and more),
     32-key segments up to kw' = 25, the per-wave kernel above that
     (kw' = min(kw, W)). The grid height decides the choice at head dim 64
     with kw' <= 9 and must be given there; depth (the grid's t extent) and
-    kernel_t matter at head dim 64 with 9 < kw' <= 13."""
+    kernel_t matter at head dim 128 with kw' <= 9 and at head dim 64 with
+    9 < kw' <= 13."""
     kw_c = min(int(kernel_w), int(width))
     if height is None:
         if int(head_dim) == 64 and kw_c <= 9:
